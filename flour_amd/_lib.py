@@ -1,0 +1,93 @@
+"""ctypes binding of libflour_hip.so (the C-ABI declared in include/flour_hip.h).
+
+The library is built in-tree by ``flour_amd.build``. Loading fails loudly when it is missing:
+there is no CPU or pure-PyTorch fallback for any operation of this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libflour_hip.so"
+
+F32, BF16, F16 = 0, 1, 2
+OK = 0
+ERR_INVALID_ARGUMENT = -1
+ERR_UNSUPPORTED = -2
+ERR_WORKSPACE = -3
+ERR_HIP = -4
+ERR_OUT_OF_BLOCKS = -5
+ERR_CAPACITY = -6
+
+_c_int, _c_i64, _c_f, _vp, _c_sz = (ctypes.c_int, ctypes.c_int64, ctypes.c_float,
+                                    ctypes.c_void_p, ctypes.c_size_t)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+# name -> (restype, argtypes); every symbol the header declares.
+SIGNATURES: dict[str, tuple] = {
+    "flour_hip_last_error": (ctypes.c_char_p, []),
+    "flour_hip_version": (ctypes.c_char_p, []),
+    "flour_hip_kv_write": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _c_int,
+                                    _c_int, _c_i64, _c_int, _vp]),
+    "flour_hip_paged_decode_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int,
+                                                       ctypes.POINTER(ctypes.c_size_t)]),
+    "flour_hip_paged_decode": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _c_int,
+                                        _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_f,
+                                        _c_int, _vp, _c_sz, _vp]),
+    "flour_hip_varlen_prefill": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp,
+                                          _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                                          _c_int, _c_int, _c_int, _c_int, _c_i64, _c_f, _c_int,
+                                          _vp]),
+}
+
+
+class FlourError(RuntimeError):
+    """An error reported by libflour_hip.so (negative return code)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libflour_hip.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("FLOUR_HIP_LIB", LIB_PATH))
+    if not path.exists():
+        raise FlourError(ERR_HIP, f"{path} is missing: build it with `python -m flour_amd.build` "
+                                  "(there is no fallback path)")
+    handle = ctypes.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    for name in EXTRA_SIGNATURES:
+        res, args = EXTRA_SIGNATURES[name]
+        fn = getattr(handle, name, None)
+        if fn is not None:
+            fn.restype = res
+            fn.argtypes = args
+    _lib = handle
+    return handle
+
+
+# Optional, non-header helpers (test / tuning switches).
+EXTRA_SIGNATURES: dict[str, tuple] = {
+    "flour_hip_set_prefill_precise_p": (_c_int, [_c_int]),
+}
+
+
+def check(code: int) -> None:
+    if code != OK:
+        msg = lib().flour_hip_last_error().decode(errors="replace")
+        raise FlourError(code, msg)
+
+
+def last_error() -> str:
+    return lib().flour_hip_last_error().decode(errors="replace")

@@ -1,0 +1,169 @@
+// flour_common.h — shared device helpers and host error plumbing for libflour_hip.so (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "flour_hip.h"
+
+namespace flour {
+
+// ------------------------------------------------------------------ vector types
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+// Tag types for the 16-bit storage formats.
+struct bf16_t {
+    uint16_t bits;
+};
+struct f16_t {
+    uint16_t bits;
+};
+
+// ------------------------------------------------------------------ scalar conversions
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float((uint32_t)x.bits << 16); }
+__device__ __forceinline__ float to_f32(f16_t x) {
+    return (float)__builtin_bit_cast(_Float16, x.bits);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) {
+    return x;
+}
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
+    // v_cvt_pk_bf16_f32 rounds to nearest even.
+    f32x2 v = {x, 0.0f};
+    bf16x2 h = __builtin_convertvector(v, bf16x2);
+    bf16_t r;
+    r.bits = __builtin_bit_cast(uint32_t, h) & 0xffffu;
+    return r;
+}
+template <>
+__device__ __forceinline__ f16_t from_f32<f16_t>(float x) {
+    f16_t r;
+    r.bits = __builtin_bit_cast(uint16_t, (_Float16)x);
+    return r;
+}
+
+// Two floats -> one dword of two 16-bit values (lo = a, hi = b), round to nearest even.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
+    f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
+    f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// The low / high 16-bit element of a dword, widened to fp32.
+template <typename T>
+__device__ __forceinline__ float lo_f32(uint32_t w);
+template <typename T>
+__device__ __forceinline__ float hi_f32(uint32_t w);
+template <>
+__device__ __forceinline__ float lo_f32<bf16_t>(uint32_t w) {
+    return __uint_as_float(w << 16);
+}
+template <>
+__device__ __forceinline__ float hi_f32<bf16_t>(uint32_t w) {
+    return __uint_as_float(w & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ float lo_f32<f16_t>(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+template <>
+__device__ __forceinline__ float hi_f32<f16_t>(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// ------------------------------------------------------------------ MFMA wrappers
+// 16x16x32 (A: 16 x 32, B: 32 x 16, 8 elements per lane), fp32 accumulate.
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<bf16_t>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<f16_t>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// 16x16x16 (4 elements per lane).
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x16<bf16_t>(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a),
+                                                     __builtin_bit_cast(bf16x4, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x16<f16_t>(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+}
+// 32x32x16 (A: 32 x 16, B: 16 x 32, 8 elements per lane), 16 fp32 per lane.
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma32x32x16<bf16_t>(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32x32x16<f16_t>(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ misc device helpers
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// dword v_perm_b32 select: bytes 0-3 come from `lo_src`, 4-7 from `hi_src`.
+__device__ __forceinline__ uint32_t perm_lo16(uint32_t lo_src, uint32_t hi_src) {
+    // result = (hi_src.lo16 << 16) | lo_src.lo16
+    return __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t perm_hi16(uint32_t lo_src, uint32_t hi_src) {
+    // result = (hi_src.hi16 << 16) | lo_src.hi16
+    return __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);
+}
+
+__device__ __forceinline__ float wave_shfl_xor(float x, int mask) {
+    return __shfl_xor(x, mask, 64);
+}
+
+// ------------------------------------------------------------------ host-side error state
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+inline int elem_bytes(int dtype) { return dtype == FLOUR_DTYPE_F32 ? 4 : 2; }
+inline bool valid_dtype(int dtype) {
+    return dtype == FLOUR_DTYPE_F32 || dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16;
+}
+
+// Check a HIP launch/runtime status; record an error and return FLOUR_ERR_HIP on failure.
+int check_hip(hipError_t e, const char* what);
+
+}  // namespace flour

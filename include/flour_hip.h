@@ -1,0 +1,133 @@
+/*
+ * flour_hip.h — C-ABI of libflour_hip.so, the MI355X (gfx950) attention hot path of flour.
+ *
+ * The library replaces the reference's CPU attention seam (reference files cited as path:line,
+ * relative to the lltsdyp/flour checkout):
+ *
+ *   src/backend/cpu.rs:57-112          paged_attention(q, blocks, n_rep, scale)
+ *   src/models/common/paged.rs:186-204 PagedKvPool::write(layer, slots, k, v)
+ *   src/models/common/paged.rs:114-121 BlockTable::slot / slots
+ *   src/models/common/paged.rs:7-54    BlockAllocator
+ *   src/models/common/paged.rs:138-167 PagedKvPool::new (device KV layout)
+ *   src/models/common/cache.rs:429-458 Cache::allocate_kv / write_kv / kv_blocks
+ *   src/models/common/cache.rs:112-159 KvCache::match_prefix / register_prefix
+ *
+ * Conventions
+ *   - Every function returns FLOUR_OK (0) on success or a negative FLOUR_ERR_* code;
+ *     flour_hip_last_error() then holds a message (per calling thread).
+ *   - Device pointers are owned by the caller. Kernel launches are asynchronous and ordered on
+ *     `stream` (a hipStream_t passed as void*; NULL = the default stream).
+ *   - The KV pool of one layer is two device arrays, K and V, each laid out
+ *     (kv_heads, num_slots, head_dim) row-major, exactly as PagedKvPool::new builds them
+ *     (paged.rs:124-167). Slot s of physical block b is b * block_size + s % block_size
+ *     (paged.rs:114-116), so the 16 rows of one (head, block) pair are contiguous.
+ *   - Element types are given by the flour_dtype codes below. Arithmetic is fp32 throughout;
+ *     bf16/f16 inputs are widened exactly, outputs are rounded to nearest-even.
+ */
+#ifndef FLOUR_HIP_H
+#define FLOUR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum flour_dtype {
+    FLOUR_DTYPE_F32 = 0,
+    FLOUR_DTYPE_BF16 = 1,
+    FLOUR_DTYPE_F16 = 2,
+};
+
+#define FLOUR_OK 0
+#define FLOUR_ERR_INVALID_ARGUMENT (-1)
+#define FLOUR_ERR_UNSUPPORTED (-2)
+#define FLOUR_ERR_WORKSPACE (-3)
+#define FLOUR_ERR_HIP (-4)
+#define FLOUR_ERR_OUT_OF_BLOCKS (-5)
+#define FLOUR_ERR_CAPACITY (-6)
+
+/* Message describing the last error on the calling thread ("" if none). */
+const char* flour_hip_last_error(void);
+
+/* Library version string. */
+const char* flour_hip_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Kernel (1): KV-cache write.
+ * Replaces PagedKvPool::write (src/models/common/paged.rs:186-204) as called through
+ * KvCache::write_current (src/models/common/cache.rs:71-77).
+ *
+ * For every token t with slot_mapping[t] >= 0 and every kv head h:
+ *     k_pool[h, slot_mapping[t], :] = k[t, h, :]     (and the same for v)
+ * where element (t, h, d) of k / v sits at t*stride_tok + h*stride_head + d (elements).
+ * The reference layout (1, kv_heads, seq, head_dim) is stride_tok = head_dim,
+ * stride_head = seq*head_dim; a packed (tokens, kv_heads, head_dim) batch is
+ * stride_tok = kv_heads*head_dim, stride_head = head_dim.
+ * A negative slot marks a padding token and is skipped; a slot >= num_slots is never written.
+ * The copy is bit-exact (no conversion): k/v and the pools share `dtype`.
+ * ---------------------------------------------------------------------------------------- */
+int flour_hip_kv_write(const void* k, const void* v, int64_t stride_tok, int64_t stride_head,
+                       void* k_pool, void* v_pool, const int32_t* slot_mapping, int num_tokens,
+                       int kv_heads, int head_dim, int64_t num_slots, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Kernel (2): paged decode attention (one new query token per sequence).
+ * Replaces paged_attention (src/backend/cpu.rs:57-112) for seq_q == 1, batched over sequences,
+ * with the block list of Cache::kv_blocks (cache.rs:456-458 -> KvCache::gather_blocks
+ * cache.rs:83-96) given as a block table.
+ *
+ *   q            (batch, num_heads, head_dim) contiguous, post-RoPE
+ *   out          (batch, num_heads, head_dim) contiguous, element type out_dtype
+ *   block_tables [batch, max_blocks_per_seq] int32 physical block ids, logical order
+ *   context_lens [batch] int32 kv length of each sequence (>= 1; 0 gives a zero row)
+ *   Query head h attends kv head h / (num_heads / kv_heads) (repeat_kv, cpu.rs:5-13).
+ *   scale multiplies q.k before the softmax (attention.rs:108 passes 1/sqrt(head_dim)).
+ *   max_context_len bounds context_lens[] and sizes the split-context grid.
+ *
+ * Long contexts are split across workgroups; partial (max, sum, acc) rows are merged by the
+ * last workgroup of each (sequence, kv head). `workspace` holds those partials plus one
+ * counter per (sequence, kv head): it must be zero-filled once when first allocated, and
+ * every call leaves the counters at zero again. Calls that share a workspace must not
+ * overlap in time. flour_hip_paged_decode_workspace_size gives the bytes required.
+ * ---------------------------------------------------------------------------------------- */
+int flour_hip_paged_decode_workspace_size(int batch, int num_heads, int kv_heads, int head_dim,
+                                          int max_context_len, size_t* bytes);
+
+int flour_hip_paged_decode(void* out, int out_dtype, const void* q, const void* k_pool,
+                           const void* v_pool, const int32_t* block_tables,
+                           int max_blocks_per_seq, const int32_t* context_lens, int batch,
+                           int num_heads, int kv_heads, int head_dim, int block_size,
+                           int64_t num_slots, int max_context_len, float scale, int dtype,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Kernel (3): causal varlen prefill attention over the paged cache.
+ * Replaces paged_attention (src/backend/cpu.rs:57-112) for seq_q >= 1, batched over packed
+ * sequences. Sequence s owns query rows cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1 and attends
+ * kv_lens[s] cached positions (its suffix plus any prefix-cached shared blocks), with the
+ * reference's causal rule (cpu.rs:68, :88-95): query i of a sequence with q_len rows sees kv
+ * position j iff j <= kv_len - q_len + i.
+ *
+ *   q    row r, head h at r*q_stride_tok + h*q_stride_head (elements), head_dim contiguous
+ *   out  row r, head h at r*o_stride_tok + h*o_stride_head, element type out_dtype
+ *   cu_seqlens_q [num_seqs+1] int32, kv_lens [num_seqs] int32 (kv_len >= q_len)
+ *   block_tables [num_seqs, max_blocks_per_seq] int32
+ *   max_seqlen_q bounds the per-sequence query count; total_q = cu_seqlens_q[num_seqs].
+ * The K/V of the new rows must already be in the pool (flour_hip_kv_write).
+ * ---------------------------------------------------------------------------------------- */
+int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stride_tok,
+                             int64_t o_stride_head, const void* q, int64_t q_stride_tok,
+                             int64_t q_stride_head, const void* k_pool, const void* v_pool,
+                             const int32_t* cu_seqlens_q, const int32_t* kv_lens,
+                             const int32_t* block_tables, int max_blocks_per_seq, int num_seqs,
+                             int max_seqlen_q, int total_q, int num_heads, int kv_heads,
+                             int head_dim, int block_size, int64_t num_slots, float scale,
+                             int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLOUR_HIP_H */

@@ -1,0 +1,153 @@
+"""Kernel (2) parity: paged decode attention against the oracle's restatement of
+paged_attention (src/backend/cpu.rs:57-112) for seq_q == 1, on identical seeded inputs.
+
+Tolerances (written here, per the path's contract):
+  * fp32 pools:                      max-abs <= 1e-5 against the fp32 oracle;
+  * bf16 pools, fp32 output:         max-abs <= 2e-3 and rel-L2 <= 1e-3 against the fp32
+                                     oracle (the kernel's fp32 accumulator, before rounding);
+  * bf16 pools, bf16 output:         exactly RNE(kernel fp32 result), and within 1 bf16 ulp of
+                                     RNE(fp32 oracle) where |ref| >= 2^-10 (1e-5 abs. below)
+                                     (rounding an exact result to bf16 alone already costs
+                                     rel-L2 ~1.6e-3, so the fp32 limits cannot apply to it).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _util import check_bf16_output, errors, to_np
+from flour_amd import ops
+from flour_amd.workloads import make_decode, make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_decode(c) -> np.ndarray:
+    B = c.q.shape[0]
+    return O.paged_attention(to_np(c.q), to_np(c.k_pool), to_np(c.v_pool), to_np(c.block_tables),
+                             np.arange(B + 1, dtype=np.int32), to_np(c.context_lens),
+                             c.block_size, c.scale, bf16=(c.q.dtype != torch.float16))
+
+
+def run(c, out_dtype=None):
+    out = ops.paged_decode(c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens, c.scale,
+                           c.max_context_len, block_size=c.block_size, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return out
+
+
+def check_bf16(c, tag=""):
+    ref = oracle_decode(c)
+    got32 = to_np(run(c, torch.float32))
+    max_abs, rel = errors(got32, ref)
+    print(f"{tag} fp32-out max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+    rep = check_bf16_output(to_np(run(c, torch.bfloat16)), got32, ref)
+    print(f"{tag} bf16-out {rep}", flush=True)
+    return max_abs, rel
+
+
+def test_decode_fp32_workload(device):
+    """fp32 decode: batch 4, 8/8 heads, head_dim 64, contexts U[1, 256]."""
+    c = make_workload("decode_f32_b4_h8_d64", device=device)
+    got = to_np(run(c))
+    ref = oracle_decode(c)
+    max_abs, _ = errors(got, ref)
+    print(f"fp32 workload max_abs={max_abs:.3e}", flush=True)
+    assert max_abs <= 1e-5
+
+
+@pytest.mark.parametrize("H,G,D,bs,ctx", [
+    (2, 2, 4, 3, [7]),            # the reference's decode-step test shape (cpu.rs:208-224)
+    (4, 2, 4, 4, [6, 1, 9]),      # GQA
+    (8, 8, 64, 16, [1, 16, 17, 255]),
+    (6, 3, 96, 5, [33, 2]),
+])
+def test_decode_fp32_small_shapes(device, H, G, D, bs, ctx):
+    c = make_decode(len(ctx), H, G, D, bs, (1, 1), dtype=torch.float32, seed=H * D + bs,
+                    device=device, context_lens=ctx)
+    max_abs, _ = errors(to_np(run(c)), oracle_decode(c))
+    assert max_abs <= 1e-5
+
+
+@pytest.mark.parametrize("H,G,ctx", [
+    (32, 8, [1, 2, 15, 16, 17, 31, 63, 64, 65, 100]),   # partial tiles, one split
+    (8, 8, [1000, 513, 2049]),                          # n_rep 1, several splits
+    (28, 4, [1500, 40, 777]),                           # n_rep 7 (Qwen2 shape)
+    (64, 8, [3000, 5]),                                 # n_rep 8
+    (16, 1, [4100, 300]),                               # n_rep 16
+])
+def test_decode_bf16_mfma_shapes(device, H, G, ctx):
+    c = make_decode(len(ctx), H, G, 128, 16, (1, 1), dtype=torch.bfloat16, seed=H + G,
+                    device=device, context_lens=ctx)
+    check_bf16(c, f"H={H} G={G}")
+
+
+def test_decode_bf16_block_size_32(device):
+    c = make_decode(3, 16, 4, 128, 32, (1, 1), dtype=torch.bfloat16, seed=77, device=device,
+                    context_lens=[31, 32, 1000])
+    check_bf16(c, "bs32")
+
+
+def test_decode_f16(device):
+    c = make_decode(3, 16, 4, 128, 16, (1, 1), dtype=torch.float16, seed=78, device=device,
+                    context_lens=[31, 600, 1000])
+    ref = oracle_decode(c)
+    max_abs, rel = errors(to_np(run(c, torch.float32)), ref)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+def test_decode_llama3_8b_workload(device):
+    """bf16 decode, batch 64, 32/8 heads, contexts U[512, 4096], 0.1% K outlier channels x20."""
+    c = make_workload("decode_bf16_llama3_8b", device=device)
+    print(f"outliers={c.meta['k_outlier_channels']}", flush=True)
+    check_bf16(c, "llama3-8b decode")
+
+
+def test_decode_long_context_workload(device):
+    """bf16 decode, batch 8, 64/8 heads, contexts U[16384, 32768] (split-context merge)."""
+    c = make_workload("decode_bf16_long_llama3_70b", device=device)
+    check_bf16(c, "long-context decode")
+
+
+def test_decode_repeat_calls_reuse_workspace(device):
+    """Split counters return to zero: repeated calls give identical results."""
+    c = make_decode(5, 32, 8, 128, 16, (2000, 5000), dtype=torch.bfloat16, seed=21, device=device)
+    ws = ops.DecodeWorkspace(device)
+    outs = []
+    for _ in range(3):
+        outs.append(ops.paged_decode(c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens,
+                                     c.scale, c.max_context_len, workspace=ws))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    counters = ws.buf[: 5 * 8 * 4].view(torch.int32)
+    assert int(counters.abs().sum().item()) == 0
+
+
+def test_decode_block_permutation_invariance(device):
+    """The same logical cache in other physical blocks gives bit-identical outputs."""
+    c = make_decode(4, 32, 8, 128, 16, (100, 3000), dtype=torch.bfloat16, seed=31, device=device)
+    a = run(c, torch.float32)
+    nb = c.k_pool.shape[1] // 16
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1)).to(device)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(nb, device=device)
+    # physical block p moves to perm[p]
+    kp = c.k_pool.view(8, nb, 16, 128)[:, inv].reshape_as(c.k_pool).contiguous()
+    vp = c.v_pool.view(8, nb, 16, 128)[:, inv].reshape_as(c.v_pool).contiguous()
+    bt = perm[c.block_tables.long()].to(torch.int32).contiguous()
+    b = ops.paged_decode(c.q, kp, vp, bt, c.context_lens, c.scale, c.max_context_len,
+                         out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_decode_empty_context_gives_zeros(device):
+    c = make_decode(2, 8, 2, 128, 16, (1, 1), dtype=torch.bfloat16, seed=3, device=device,
+                    context_lens=[0, 5])
+    out = to_np(run(c, torch.float32))
+    assert not out[0].any()
+    ref = oracle_decode(c)
+    assert errors(out[1], ref[1])[0] <= 2e-3

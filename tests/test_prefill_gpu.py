@@ -1,0 +1,150 @@
+"""Kernels (1)+(3) parity: KV write then causal varlen prefill attention against the oracle's
+restatement of paged_attention (src/backend/cpu.rs:57-112) for seq_q >= 1, including suffixes
+over prefix-cached shared blocks, on identical seeded inputs.
+
+Tolerances: fp32 pools max-abs <= 1e-5; bf16 pools with fp32 output max-abs <= 2e-3 and
+rel-L2 <= 1e-3 against the fp32 oracle; bf16 output exactly RNE(kernel fp32 result) and
+within 1 bf16 ulp of RNE(fp32 oracle) where |ref| >= 2^-10 (1e-5 absolute below).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _util import check_bf16_output, errors, to_np
+from flour_amd import ops
+from flour_amd.workloads import make_prefill, make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+def write(c):
+    ops.kv_write(c.k_new, c.v_new, c.k_pool, c.v_pool, c.slot_mapping)
+
+
+def run(c, out_dtype=None, q=None):
+    out = ops.varlen_prefill(c.q if q is None else q, c.k_pool, c.v_pool, c.cu_seqlens_q,
+                             c.kv_lens, c.block_tables, c.max_seqlen_q, c.scale,
+                             block_size=c.block_size, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle_prefill(c, seqs=None) -> tuple[np.ndarray, np.ndarray]:
+    """Oracle output for the listed sequences; returns (reference, packed row indices)."""
+    cu = to_np(c.cu_seqlens_q)
+    n = cu.size - 1
+    seqs = list(range(n)) if seqs is None else list(seqs)
+    rows = np.concatenate([np.arange(cu[s], cu[s + 1]) for s in seqs])
+    sub_cu = np.concatenate([[0], np.cumsum([cu[s + 1] - cu[s] for s in seqs])]).astype(np.int32)
+    ref = O.paged_attention(to_np(c.q)[rows], to_np(c.k_pool), to_np(c.v_pool),
+                            to_np(c.block_tables)[seqs], sub_cu, to_np(c.kv_lens)[seqs],
+                            c.block_size, c.scale, bf16=(c.q.dtype != torch.float16))
+    return ref, rows
+
+
+def check_bf16(c, seqs=None, tag=""):
+    ref, rows = oracle_prefill(c, seqs)
+    got32 = to_np(run(c, torch.float32))[rows]
+    max_abs, rel = errors(got32, ref)
+    print(f"{tag} fp32-out max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+    rep = check_bf16_output(to_np(run(c, torch.bfloat16))[rows], got32, ref)
+    print(f"{tag} bf16-out {rep}", flush=True)
+
+
+@pytest.mark.parametrize("H,G,D,bs,lens,prefix", [
+    (2, 2, 4, 2, [5], 0),          # the reference's prefill test shape (cpu.rs:190-206)
+    (4, 2, 4, 4, [6], 0),          # GQA (cpu.rs:226-242)
+    (4, 1, 8, 4, [3, 5], 16),      # suffixes over a cached prefix
+    (8, 8, 64, 16, [1, 17, 40], 32),
+])
+def test_prefill_fp32_small_shapes(device, H, G, D, bs, lens, prefix):
+    c = make_prefill(len(lens), H, G, D, bs, (1, 1), prefix=prefix, dtype=torch.float32,
+                     seed=H + D, device=device, q_lens=lens)
+    write(c)
+    ref, rows = oracle_prefill(c)
+    max_abs, _ = errors(to_np(run(c))[rows], ref)
+    assert max_abs <= 1e-5
+
+
+@pytest.mark.parametrize("H,G,lens,prefix", [
+    (8, 2, [1, 2, 31, 32, 33], 0),
+    (32, 8, [64, 127, 128, 129, 300], 0),
+    (28, 4, [130, 17], 1024),      # n_rep 7, cached prefix (Qwen2 shape)
+    (16, 16, [257, 5], 48),        # n_rep 1
+    (8, 1, [1, 200], 160),
+])
+def test_prefill_bf16_mfma_shapes(device, H, G, lens, prefix):
+    c = make_prefill(len(lens), H, G, 128, 16, (1, 1), prefix=prefix, dtype=torch.bfloat16,
+                     seed=H * 3 + G, device=device, q_lens=lens)
+    write(c)
+    check_bf16(c, tag=f"H={H} G={G} lens={lens} prefix={prefix}")
+
+
+def test_prefill_varlen_llama3_8b_workload(device):
+    """KV write + causal varlen prefill, 8 sequences U[256, 2048], 32/8 heads."""
+    c = make_workload("prefill_bf16_varlen_llama3_8b", device=device)
+    write(c)
+    lens = (c.cu_seqlens_q[1:] - c.cu_seqlens_q[:-1]).tolist()
+    print(f"lens={lens} causal_pairs={c.causal_pairs()}", flush=True)
+    order = np.argsort(lens)
+    check_bf16(c, seqs=[int(order[0]), int(order[-1])], tag="llama3-8b prefill")
+
+
+def test_prefill_prefix_qwen2_7b_workload(device):
+    """Prefix-cached prefill: 16 suffixes U[128, 512] over one shared 1024-token prefix."""
+    c = make_workload("prefill_bf16_prefix_qwen2_7b", device=device)
+    write(c)
+    check_bf16(c, seqs=[0, 7, 15], tag="qwen2-7b prefix prefill")
+
+
+def test_suffix_over_cached_prefix_matches_cold_prefill(device):
+    """model.rs:244-360 at the attention level: the suffix rows of a cold full prefill equal a
+    suffix-only prefill over the cached prefix blocks."""
+    P, S, H, G = 96, 70, 8, 2
+    cold = make_prefill(1, H, G, 128, 16, (1, 1), prefix=0, dtype=torch.bfloat16, seed=12,
+                        device=device, q_lens=[P + S])
+    write(cold)
+    full = run(cold, torch.float32)
+    # the same sequence: prefix rows already cached, only the last S rows are new queries
+    cu = torch.tensor([0, S], dtype=torch.int32, device=device)
+    kvl = torch.tensor([P + S], dtype=torch.int32, device=device)
+    out = ops.varlen_prefill(cold.q[P:], cold.k_pool, cold.v_pool, cu, kvl, cold.block_tables,
+                             S, cold.scale, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert errors(to_np(out), to_np(full[P:]))[0] <= 1e-5
+
+
+def test_prefill_reference_layout_and_strided_output(device):
+    """q in the reference's head-major (H, seq, D) layout as a transposed view; strided out."""
+    c = make_prefill(1, 16, 4, 128, 16, (1, 1), dtype=torch.bfloat16, seed=8, device=device,
+                     q_lens=[150])
+    write(c)
+    q_ref = c.q.transpose(0, 1).contiguous()       # (H, S, D)
+    out_ref = torch.empty((16, 150, 128), dtype=torch.float32, device=device)
+    ops.varlen_prefill(q_ref.transpose(0, 1), c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                       c.block_tables, c.max_seqlen_q, c.scale, out_dtype=torch.float32,
+                       out=out_ref.transpose(0, 1))
+    torch.cuda.synchronize()
+    packed = run(c, torch.float32)
+    assert torch.equal(out_ref.transpose(0, 1), packed)
+
+
+def test_prefill_single_rounding_mode_still_within_bf16_output_bound(device):
+    """The optional single-rounding P mode (faster) keeps bf16 outputs within 1 ulp."""
+    from flour_amd import _lib
+    c = make_prefill(3, 32, 8, 128, 16, (1, 1), dtype=torch.bfloat16, seed=5, device=device,
+                     q_lens=[300, 64, 1000])
+    write(c)
+    ref, rows = oracle_prefill(c)
+    _lib.lib().flour_hip_set_prefill_precise_p(0)
+    try:
+        got = to_np(run(c, torch.float32))[rows]
+    finally:
+        _lib.lib().flour_hip_set_prefill_precise_p(1)
+    max_abs, rel = errors(got, ref)
+    print(f"single-rounding P: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-2
