@@ -80,6 +80,7 @@ def lib() -> ctypes.CDLL:
 # Optional, non-header helpers (test / tuning switches).
 EXTRA_SIGNATURES: dict[str, tuple] = {
     "flour_hip_set_prefill_precise_p": (_c_int, [_c_int]),
+    "flour_hip_set_decode_workgroups": (_c_int, [_c_int]),
 }
 
 

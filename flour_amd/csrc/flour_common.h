@@ -137,6 +137,12 @@ __device__ __forceinline__ f32x16 mfma32x32x16<f16_t>(u32x4 a, u32x4 b, f32x16 c
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// ------------------------------------------------------------------ buffer loads
+// Dword 3 of a raw buffer resource (untyped 32-bit data format) and the cache-policy bits of
+// a non-temporal load.
+static constexpr int BUF_DWORD3 = 0x00020000;
+static constexpr int BUF_NT = 2;
+
 // ------------------------------------------------------------------ misc device helpers
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -152,6 +158,26 @@ __device__ __forceinline__ uint32_t perm_hi16(uint32_t lo_src, uint32_t hi_src) 
 
 __device__ __forceinline__ float wave_shfl_xor(float x, int mask) {
     return __shfl_xor(x, mask, 64);
+}
+
+// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48) with the gfx950
+// row-swap instructions (plain VALU ops, no LDS crossbar): permlane16_swap pairs lane l with
+// l^16, permlane32_swap pairs l with l^32.
+__device__ __forceinline__ float max_across_rows(float x) {
+    const uint32_t u = __float_as_uint(x);
+    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t v = __float_as_uint(x);
+    auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_across_rows(float x) {
+    const uint32_t u = __float_as_uint(x);
+    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const uint32_t v = __float_as_uint(x);
+    auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // ------------------------------------------------------------------ host-side error state

@@ -7,29 +7,39 @@
 // the causal mask of cpu.rs:88-95 admits every cached position, so only positions past the
 // context length are masked.
 //
-// Design (bf16/f16 pools, head_dim 128, block_size a multiple of 16):
-//  * One workgroup of 4 waves per (context split, kv head, sequence). Every wave handles
-//    16-token tiles (one MFMA tile; one 4 KB (head, 16 slots) pool run of K and of V) with a
-//    stride of 4 tiles, so the 4 waves stream adjacent pool memory. All n_rep query heads of
-//    the kv head share each K/V load (GQA reuse: K/V are read from HBM once).
+// Work decomposition (stream-K): the K/V to read is the list of 32-token chunks of every
+// (sequence, kv head) pair, laid end to end. One resident round of workgroups (2 per CU) each
+// takes an equal contiguous range of that list, so every CU streams the same number of bytes
+// whatever the spread of context lengths, and no workgroup pays a launch or a ramp-up twice.
+// A pair wholly inside one range is finished by its workgroup; a pair cut by range ends leaves
+// one partial (max, sum, acc) row per piece, and a small second kernel on the same stream
+// merges those (log-sum-exp merge, as in the running update of cpu.rs:96-105). The kernel
+// boundary orders partial writes before merge reads; an in-kernel "last workgroup merges"
+// scheme would need an agent-scope release/acquire per workgroup, which on this multi-XCD part
+// writes back and invalidates the XCD's L2 each time.
+//
+// Inside a piece (bf16/f16 pools, head_dim 128, block_size a multiple of 16):
+//  * The 4 waves take the piece's chunks round robin. A chunk is two 16-token MFMA tiles, each
+//    one 4 KB (head, 16 slots) pool run of K and of V, read with non-temporal buffer loads
+//    (per-pool resource, loop-invariant lane offset, per-tile SGPR offset); two register
+//    buffers ping-pong so the next chunk's loads are in flight while one is computed. Every
+//    query head of the kv head shares each K/V load (GQA reuse: K/V leave HBM once).
 //  * Scores S = K Q^T on v_mfma_f32_16x16x32 (M = 16 tokens, N = 16 query-head columns, the
-//    n_rep real heads padded with zero rows), so lane (g, c) = (lane/16, lane%16) holds the
-//    scores of query head c for tokens 4g..4g+3.
-//  * That register layout is exactly the B operand of v_mfma_f32_16x16x16 for O^T = V^T P^T
-//    (K = the 16 tokens), so P never leaves the lane. The V^T A operand is built in-lane:
-//    each lane loads V rows 4g..4g+3, dims 8c..8c+7 (four fully coalesced 16 B loads; a wave
-//    reads 4 whole 256 B rows per instruction) and v_perm_b32 packs, per output dim 8c+n,
-//    the four tokens' values. The O^T accumulator then holds, in lane (g, c), query head c at
-//    dims 32g..32g+31.
-//  * P is split into bf16 hi + lo parts (two MFMAs per product) so the P.V contraction keeps
+//    n_rep real heads padded with zero rows): lane (g, c) = (lane/16, lane%16) holds head c's
+//    scores for tokens 4g..4g+3 of each tile.
+//  * Those registers, for the two tiles, are exactly the B operand of v_mfma_f32_16x16x32 for
+//    O^T = V^T P^T (K = the 32 tokens), so P never leaves the lane. The V^T A operand is built
+//    in-lane: each lane loads V rows 4g..4g+3, dims 8c..8c+7 (a wave reads 4 whole 256 B rows
+//    per instruction) and v_perm_b32 packs, per output dim 8c+n, the four tokens' values. The
+//    O^T accumulator holds, in lane (g, c), query head c at dims 32g..32g+31.
+//  * P is split into hi + lo 16-bit parts (two MFMAs per product) so the P.V contraction keeps
 //    ~16 mantissa bits of P; products are exact in fp32 and accumulate in fp32.
-//  * Online softmax in the exp2 domain: the only cross-lane step per tile is the max over the
-//    four 4-token row groups (two xor shuffles); running sums stay lane-partial until the
-//    end, and the accumulator is rescaled only when some lane's max moved.
-//  * Split-context: partial (max, sum, acc) rows go to the workspace; the last workgroup of a
-//    (sequence, kv head) — elected with an atomic counter it resets — merges them (log-sum-
-//    exp merge, as in the running update of cpu.rs:96-105) and writes the output.
+//  * Online softmax in the exp2 domain: the only cross-lane step per chunk is the max over the
+//    four row groups (two v_permlane*_swap exchanges); running sums stay lane-partial until
+//    the end, and the accumulator is rescaled only when some lane's max moved.
 #include <math.h>
+
+#include <type_traits>
 
 #include "flour_common.h"
 
@@ -43,265 +53,502 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
                         float scale, hipStream_t stream);
 
 static constexpr int DEC_D = 128;
-static constexpr int DEC_WAVES = 4;
-static constexpr int DEC_THREADS = DEC_WAVES * 64;
 static constexpr float LOG2E = 1.4426950408889634f;
 
+static constexpr int DEC_CHUNK = 32;         // tokens per step (two 16-token MFMA tiles)
+static constexpr int DEC_SEG = 32;           // chunks per tile-slot refill (64 tiles, one per lane)
+static constexpr int DEC_MAX_BATCH = 4096;   // per-sequence chunk prefix sums live in LDS
+static constexpr int DEC_WAVES_PER_CU = 8;
+// K rows are read as two 64 B halves of each 128 B line by back-to-back instructions; a
+// cached load lets the second half hit the line the first brought in, which measures faster
+// than the non-temporal hint that suits the fully coalesced V rows.
+#ifndef FLOUR_DEC_K_POLICY
+#define FLOUR_DEC_K_POLICY 0
+#endif
+static constexpr int K_POLICY = FLOUR_DEC_K_POLICY;   // 2 per SIMD: the register budget of the kernel
+
 struct DecodeWs {
-    int* counters;  // [batch * kv_heads]
-    float* ml;      // [batch * kv_heads * max_splits * n_rep][2] (max, sum), exp2 domain
-    float* o;       // [batch * kv_heads * max_splits * n_rep * D]
+    float* ml;  // [2 * num_waves][n_rep][2] (max, sum) in the exp2 domain
+    float* o;   // [2 * num_waves][n_rep][D]
 };
 
-// Tokens per context split: a multiple of 64 (4 waves x 16-token tiles). Long contexts use
-// 512-token splits; short or few sequences use smaller splits so the grid fills the 256 CUs.
-static int choose_split_tokens(int batch, int kv_heads, int max_context_len) {
-    int split = 512;
-    const int64_t units = (int64_t)batch * kv_heads;
-    while (split > 64 && units * ((max_context_len + split - 1) / split) < 1024) split >>= 1;
-    return split;
+static int g_wg_override = 0;  // tuning / test hook: number of waves (0 = one resident round)
+
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+static int decode_workgroups() {
+    const int n = g_wg_override > 0 ? g_wg_override : device_cus() * DEC_WAVES_PER_CU;
+    return n < 4096 ? n : 4096;
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static size_t decode_ws_bytes(int batch, int kv_heads, int n_rep, int head_dim, int max_splits) {
-    const size_t units = (size_t)batch * kv_heads;
-    return align256(units * sizeof(int)) + align256(units * max_splits * n_rep * 2 * sizeof(float)) +
-           align256(units * max_splits * n_rep * (size_t)head_dim * sizeof(float));
+static size_t decode_ws_bytes(int nwg, int n_rep, int head_dim) {
+    const size_t slots = 2 * (size_t)nwg;
+    return align256(slots * n_rep * 2 * sizeof(float)) +
+           align256(slots * n_rep * (size_t)head_dim * sizeof(float));
 }
 
-template <typename T, typename TO>
-__global__ __launch_bounds__(DEC_THREADS) void paged_decode_mfma_kernel(
+__device__ __forceinline__ int decode_chunks(int ctx, int max_ctx) {
+    ctx = min(ctx, max_ctx);
+    return ctx > 0 ? (ctx + DEC_CHUNK - 1) / DEC_CHUNK : 0;
+}
+
+// Range owner of flattened chunk x when `total` chunks are cut into `n` ranges
+// [floor(i * total / n), floor((i + 1) * total / n)).
+__device__ __forceinline__ int64_t owner_wg(int64_t x, int64_t total, int64_t n) {
+    return ((x + 1) * n + total - 1) / total - 1;
+}
+
+// One wave per workgroup; each wave owns one contiguous range of the chunk list.
+template <typename T, typename TO, bool BS16>
+__global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     TO* __restrict__ out, const T* __restrict__ q, const T* __restrict__ k_pool,
     const T* __restrict__ v_pool, const int32_t* __restrict__ block_tables, int max_blocks,
-    const int32_t* __restrict__ context_lens, int num_heads, int kv_heads, int n_rep,
-    int block_size, int64_t num_slots, int max_ctx, float scale_log2, int split_tokens,
-    int max_splits, DecodeWs ws) {
+    const int32_t* __restrict__ context_lens, int batch, int num_heads, int kv_heads, int n_rep,
+    int block_size, int64_t num_slots, int max_ctx, float scale_log2, DecodeWs ws) {
     constexpr int D = DEC_D;
-    extern __shared__ float smem[];  // [4 waves][n_rep][D] acc, then [4][n_rep] max, sum
+    extern __shared__ int pre[];  // pre[b] = chunks of sequences 0..b-1; pre[batch] = all
+    const int lane = threadIdx.x, lg = lane >> 4, lc = lane & 15;
 
-    const int sp = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
-    // Context lengths beyond the stated maximum are clamped, so a bad length can neither read
-    // past the block table nor leave a split unmerged.
-    const int ctx = min(context_lens[b], max_ctx);
-    const int n_splits = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 1;
-    if (sp >= n_splits) return;
-
-    TO* out_g = out + ((int64_t)b * num_heads + (int64_t)g * n_rep) * D;
-    if (ctx <= 0) {  // empty context: the row is defined as zeros
-        for (int idx = tid; idx < n_rep * D; idx += DEC_THREADS) out_g[idx] = from_f32<TO>(0.0f);
-        return;
+    // ---- exclusive prefix sum of per-sequence chunk counts (each lane scans a slice)
+    {
+        const int per = (batch + 63) / 64;
+        int local = 0;
+        for (int i = 0; i < per; i++) {
+            const int b = lane * per + i;
+            if (b < batch) local += decode_chunks(context_lens[b], max_ctx);
+        }
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        int run = incl - local;
+        for (int i = 0; i < per; i++) {
+            const int b = lane * per + i;
+            if (b < batch) {
+                pre[b] = run;
+                run += decode_chunks(context_lens[b], max_ctx);
+            }
+        }
+        if (lane == 63) pre[batch] = incl;
+        __syncthreads();
     }
+    const int64_t total = (int64_t)kv_heads * pre[batch];
+    const int64_t nwg = gridDim.x, wgi = blockIdx.x;
+    const int64_t lo = wgi * total / nwg, hi = (wgi + 1) * total / nwg;
 
+    if (lo >= hi) return;
+
+    const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
+    const uint32_t k_off = (uint32_t)((lc * D + 8 * lg) * sizeof(T));
+    const uint32_t v_off = (uint32_t)((4 * lg * D + 8 * lc) * sizeof(T));
+    const int64_t max_phys = num_slots / block_size - 1;
+
+    // The wave's range is a stream of segments: up to DEC_SEG consecutive chunks of one
+    // (sequence, kv head) pair. Consecutive segments of the same pair form one piece.
+    struct Seg {
+        int b, g, cb, ce, nch, tok_end;
+    };
+    auto seg_at = [&](int64_t x) -> Seg {
+        int l0 = 0, h0 = batch;  // largest b with kv_heads * pre[b] <= x
+        while (h0 - l0 > 1) {
+            const int mid = (l0 + h0) >> 1;
+            if ((int64_t)kv_heads * pre[mid] <= x)
+                l0 = mid;
+            else
+                h0 = mid;
+        }
+        Seg sg;
+        sg.b = l0;
+        sg.nch = pre[l0 + 1] - pre[l0];
+        const int64_t rel = x - (int64_t)kv_heads * pre[l0];
+        sg.g = (int)(rel / sg.nch);
+        sg.cb = (int)(rel - (int64_t)sg.g * sg.nch);
+        sg.ce = (int)min(min((int64_t)sg.nch, (int64_t)sg.cb + DEC_SEG), sg.cb + (hi - x));
+        sg.tok_end = min(min(context_lens[sg.b], max_ctx), sg.ce * DEC_CHUNK);
+        return sg;
+    };
+    // Pool slot of the first token of each tile of a segment: lane i holds tile i (chunk
+    // cb + i/2, half i%2), so the loop fetches it with v_readlane. Tiles past the segment are
+    // clamped to its last tile: every address stays valid, their tokens are masked and their V
+    // zeroed in compute_chunk.
+    auto seg_slots = [&](const Seg& sg) -> int {
+        const int32_t* bt = block_tables + (int64_t)sg.b * max_blocks;
+        const int last_tile_tok0 = ((sg.tok_end - 1) >> 4) << 4;
+        const int tok0 = min(sg.cb * DEC_CHUNK + lane * 16, last_tile_tok0);
+        const int lb = BS16 ? (tok0 >> 4) : tok0 / block_size;
+        int64_t phys = bt[lb];  // clamped: a bad block id never leaves the pool
+        phys = phys < 0 ? 0 : (phys > max_phys ? max_phys : phys);
+        return (int)(phys * block_size + (tok0 - lb * block_size));
+    };
+    // Chunk loads as buffer loads: one resource per pool (the kv head's region), the
+    // loop-invariant lane offset (VGPR) and the tile's byte offset (SGPR), so there is no
+    // per-lane address arithmetic in the loop; non-temporal (K/V are read exactly once);
+    // an out-of-region offset reads zeros instead of faulting.
+    auto load_chunk = [&](int g, int slots, int tile0, u32x4 (*kd)[4], u32x4 (*vd)[4]) {
+        const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(k_pool + (int64_t)g * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
+        const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(v_pool + (int64_t)g * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint32_t soff =
+                (uint32_t)__builtin_amdgcn_readlane(slots, tile0 + t) * (uint32_t)(D * sizeof(T));
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                kd[t][kk] = __builtin_amdgcn_raw_buffer_load_b128(
+                    k_rsrc, k_off + 32 * kk * (uint32_t)sizeof(T), soff, K_POLICY);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                vd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                    v_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
+        }
+    };
     // Q^T as the B operand: lane (lg, lc) holds head lc, dims 32kk + 8lg .. +7.
     u32x4 qb[4];
-    {
+    auto load_q = [&](int b, int g) {
         const T* qh = q + ((int64_t)b * num_heads + (int64_t)g * n_rep + lc) * D + 8 * lg;
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
+        for (int kk = 0; kk < 4; kk++)
             qb[kk] = (lc < n_rep) ? *reinterpret_cast<const u32x4*>(qh + 32 * kk) : u32x4{0, 0, 0, 0};
-        }
-    }
-
-    const int tok_begin = sp * split_tokens;
-    const int tok_end = min(ctx, tok_begin + split_tokens);
-    const int ntiles = (tok_end - tok_begin + 15) >> 4;
-    const int32_t* bt = block_tables + (int64_t)b * max_blocks;
-    const T* k_head = k_pool + (int64_t)g * num_slots * D;
-    const T* v_head = v_pool + (int64_t)g * num_slots * D;
-    const int64_t max_phys = num_slots / block_size - 1;
+    };
 
     float m = -INFINITY, lsum = 0.0f;
     f32x4 acc[8];
 #pragma unroll
     for (int nn = 0; nn < 8; nn++) acc[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    u32x4 ka[4], va[4];
-    auto load_tile = [&](int it, u32x4* kd, u32x4* vd) {
-        const int tok0 = tok_begin + it * 16;
-        const int lb = tok0 / block_size;
-        const int within = tok0 - lb * block_size;
-        int64_t phys = bt[lb];  // clamped: a bad block id never leaves the pool
-        phys = phys < 0 ? 0 : (phys > max_phys ? max_phys : phys);
-        const int64_t slot0 = phys * block_size + within;
-        const T* kp = k_head + slot0 * D;
-        const T* vp = v_head + slot0 * D;
+    auto compute_chunk = [&](int c, int tok_end, u32x4 (*ka)[4], u32x4 (*va)[4]) {
+        const int tok0 = c * DEC_CHUNK;
+        const bool full = tok0 + DEC_CHUNK <= tok_end;
+        if (!full) {  // tokens past the context: zero V so garbage bits cannot leak in
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++)
-            kd[kk] = *reinterpret_cast<const u32x4*>(kp + lc * D + 32 * kk + 8 * lg);
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            vd[j] = *reinterpret_cast<const u32x4*>(vp + (4 * lg + j) * D + 8 * lc);
-    };
-
-    int it = w;
-    if (it < ntiles) load_tile(it, ka, va);
-    for (; it < ntiles; it += DEC_WAVES) {
-        u32x4 kn[4], vn[4];
-        const int nxt = it + DEC_WAVES;
-        if (nxt < ntiles) load_tile(nxt, kn, vn);
-
-        const int tok0 = tok_begin + it * 16;
-        const bool full = tok0 + 16 <= tok_end;
-        if (!full) {  // tokens past the context: zero V so garbage pool bits cannot leak in
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (tok0 + 4 * lg + j >= tok_end) va[j] = u32x4{0, 0, 0, 0};
+                for (int j = 0; j < 4; j++)
+                    if (tok0 + 16 * t + 4 * lg + j >= tok_end) va[t][j] = u32x4{0, 0, 0, 0};
         }
-
-        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+        // S tiles: s[t][r] = score of head lc for token 16t + 4lg + r of the chunk.
+        f32x4 s[2];
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) s = mfma16x16x32<T>(ka[kk], qb[kk], s);
-
-        float sv[4];
+        for (int t = 0; t < 2; t++) {
+            s[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) s[t] = mfma16x16x32<T>(ka[t][kk], qb[kk], s[t]);
+        }
+        float sv[8];
         float tmax = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const bool ok = full || (tok0 + 4 * lg + r < tok_end);
-            sv[r] = ok ? s[r] * scale_log2 : -INFINITY;
-            tmax = fmaxf(tmax, sv[r]);
-        }
-        tmax = fmaxf(tmax, wave_shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const bool ok = full || (tok0 + 16 * t + 4 * lg + r < tok_end);
+                sv[4 * t + r] = ok ? s[t][r] * scale_log2 : -INFINITY;
+                tmax = fmaxf(tmax, sv[4 * t + r]);
+            }
+        tmax = max_across_rows(tmax);
         const float m_new = fmaxf(m, tmax);
         const float alpha = fast_exp2(m - m_new);
-        float p[4];
+        float p[8];
 #pragma unroll
-        for (int r = 0; r < 4; r++) p[r] = fast_exp2(sv[r] - m_new);
-        lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        for (int i = 0; i < 8; i++) p[i] = fast_exp2(sv[i] - m_new);
+        lsum = lsum * alpha +
+               (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
         if (__builtin_amdgcn_ballot_w64(m_new > m) != 0) {
 #pragma unroll
             for (int nn = 0; nn < 8; nn++) acc[nn] *= alpha;
         }
         m = m_new;
-
-        // P^T as B operand, split hi + lo.
-        const uint32_t ph0 = pack2<T>(p[0], p[1]), ph1 = pack2<T>(p[2], p[3]);
-        const uint32_t pl0 = pack2<T>(p[0] - lo_f32<T>(ph0), p[1] - hi_f32<T>(ph0));
-        const uint32_t pl1 = pack2<T>(p[2] - lo_f32<T>(ph1), p[3] - hi_f32<T>(ph1));
-        const u32x2 PH = {ph0, ph1}, PL = {pl0, pl1};
-
+        // P^T as the B operand over the 32 tokens: lane (lg, lc) holds head lc at
+        // k-slots 8lg + j: j < 4 -> token 4lg + j (tile 0), j >= 4 -> 16 + 4lg + j - 4.
+        // Split hi + lo so the product keeps ~16 mantissa bits of P.
+        u32x4 PH, PL;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t hi16 = pack2<T>(p[2 * i], p[2 * i + 1]);
+            PH[i] = hi16;
+            PL[i] = pack2<T>(p[2 * i] - lo_f32<T>(hi16), p[2 * i + 1] - hi_f32<T>(hi16));
+        }
+        // V^T as the A operand: lane (lg, lc) holds output dim 8lc + nn at the same
+        // k-slots, packed in-lane from its four V rows of each tile.
 #pragma unroll
         for (int nn = 0; nn < 8; nn++) {
             const int wd = nn >> 1;
-            u32x2 A;
-            if (nn & 1) {
-                A[0] = perm_hi16(va[0][wd], va[1][wd]);
-                A[1] = perm_hi16(va[2][wd], va[3][wd]);
-            } else {
-                A[0] = perm_lo16(va[0][wd], va[1][wd]);
-                A[1] = perm_lo16(va[2][wd], va[3][wd]);
+            u32x4 A;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                if (nn & 1) {
+                    A[2 * t] = perm_hi16(va[t][0][wd], va[t][1][wd]);
+                    A[2 * t + 1] = perm_hi16(va[t][2][wd], va[t][3][wd]);
+                } else {
+                    A[2 * t] = perm_lo16(va[t][0][wd], va[t][1][wd]);
+                    A[2 * t + 1] = perm_lo16(va[t][2][wd], va[t][3][wd]);
+                }
             }
-            acc[nn] = mfma16x16x16<T>(A, PH, acc[nn]);
-            acc[nn] = mfma16x16x16<T>(A, PL, acc[nn]);
+            acc[nn] = mfma16x16x32<T>(A, PH, acc[nn]);
+            acc[nn] = mfma16x16x32<T>(A, PL, acc[nn]);
         }
+    };
 
-        if (nxt < ntiles) {
+    // Piece epilogue from registers: lane (lg, lc) holds head lc, dims 32lg + 8r + nn.
+    auto epilogue = [&](int b, int g, bool complete, bool first_piece) {
+        lsum = sum_across_rows(lsum);
+        if (lc < n_rep) {
+            if (complete) {  // whole pair in this range: final output
+                TO* o = out + ((int64_t)b * num_heads + (int64_t)g * n_rep + lc) * D + 32 * lg;
+                const float inv = 1.0f / lsum;
 #pragma unroll
-            for (int x = 0; x < 4; x++) {
-                ka[x] = kn[x];
-                va[x] = vn[x];
-            }
-        }
-    }
-
-    // Wave totals: the row sum over the four row groups (max is already shared).
-    lsum += wave_shfl_xor(lsum, 16);
-    lsum += wave_shfl_xor(lsum, 32);
-
-    float* sm_o = smem;                                  // [4][n_rep][D]
-    float* sm_m = smem + DEC_WAVES * n_rep * D;          // [4][n_rep]
-    float* sm_l = sm_m + DEC_WAVES * n_rep;              // [4][n_rep]
-    if (lc < n_rep) {
-        float* o = sm_o + (w * n_rep + lc) * D + 32 * lg;
+                for (int r = 0; r < 4; r++) {
+                    if constexpr (sizeof(TO) == 4) {
+                        *reinterpret_cast<f32x4*>(o + 8 * r) =
+                            f32x4{acc[0][r] * inv, acc[1][r] * inv, acc[2][r] * inv, acc[3][r] * inv};
+                        *reinterpret_cast<f32x4*>(o + 8 * r + 4) =
+                            f32x4{acc[4][r] * inv, acc[5][r] * inv, acc[6][r] * inv, acc[7][r] * inv};
+                    } else {
+                        u32x4 v;
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+                        for (int i = 0; i < 4; i++)
+                            v[i] = pack2<TO>(acc[2 * i][r] * inv, acc[2 * i + 1][r] * inv);
+                        *reinterpret_cast<u32x4*>(o + 8 * r) = v;
+                    }
+                }
+            } else {  // partial row for the merge kernel
+                const int64_t pidx = (2 * wgi + (first_piece ? 0 : 1)) * n_rep + lc;
+                float* o = ws.o + pidx * D + 32 * lg;
 #pragma unroll
-            for (int nn = 0; nn < 8; nn++) o[8 * r + nn] = acc[nn][r];
-        if (lg == 0) {
-            sm_m[w * n_rep + lc] = m;
-            sm_l[w * n_rep + lc] = lsum;
-        }
-    }
-    __syncthreads();
-
-    const int unit = b * kv_heads + g;
-    for (int idx = tid; idx < n_rep * D; idx += DEC_THREADS) {
-        const int hh = idx / D, d = idx - hh * D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int x = 0; x < DEC_WAVES; x++) M = fmaxf(M, sm_m[x * n_rep + hh]);
-        float L = 0.0f, O = 0.0f;
-#pragma unroll
-        for (int x = 0; x < DEC_WAVES; x++) {
-            const float mx = sm_m[x * n_rep + hh];
-            const float f = (mx == -INFINITY) ? 0.0f : fast_exp2(mx - M);
-            L += f * sm_l[x * n_rep + hh];
-            O += f * sm_o[(x * n_rep + hh) * D + d];
-        }
-        if (n_splits == 1) {
-            out_g[idx] = from_f32<TO>(O / L);
-        } else {
-            const int64_t pidx = ((int64_t)unit * max_splits + sp) * n_rep + hh;
-            ws.o[pidx * D + d] = O;
-            if (d == 0) {
-                ws.ml[2 * pidx] = M;
-                ws.ml[2 * pidx + 1] = L;
+                for (int r = 0; r < 4; r++) {
+                    *reinterpret_cast<f32x4*>(o + 8 * r) =
+                        f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+                    *reinterpret_cast<f32x4*>(o + 8 * r + 4) =
+                        f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+                }
+                if (lg == 0) {
+                    ws.ml[2 * pidx] = m;
+                    ws.ml[2 * pidx + 1] = lsum;
+                }
             }
         }
-    }
-    if (n_splits == 1) return;
+        m = -INFINITY;
+        lsum = 0.0f;
+#pragma unroll
+        for (int nn = 0; nn < 8; nn++) acc[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
 
-    // Split-context merge: the last workgroup of this (sequence, kv head) combines partials.
-    __shared__ int sm_last;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const int prev = atomicAdd(&ws.counters[unit], 1);
-        sm_last = (prev == n_splits - 1);
+    // ---- the chunk stream. The next segment's block-table slots are read while the current
+    // one streams, and the two register buffers ping-pong across segment and piece boundaries:
+    // the next chunk's loads (chosen with uniform selects, never a branch, so the compiler's
+    // wait counts stay exact) are in flight while the current chunk is computed and while a
+    // finished piece is written out.
+    Seg cur = seg_at(lo);
+    int cur_slots = seg_slots(cur);
+    int64_t nx = lo + (cur.ce - cur.cb);
+    bool has_nxt = nx < hi;
+    Seg nxt = cur;
+    int nxt_slots = cur_slots;
+    if (has_nxt) {
+        nxt = seg_at(nx);
+        nxt_slots = seg_slots(nxt);
     }
-    __syncthreads();
-    if (!sm_last) return;
-    __threadfence();
-    for (int idx = tid; idx < n_rep * D; idx += DEC_THREADS) {
-        const int hh = idx / D, d = idx - hh * D;
-        const int64_t base = (int64_t)unit * max_splits * n_rep + hh;
-        float M = -INFINITY;
-        for (int x = 0; x < n_splits; x++) M = fmaxf(M, ws.ml[2 * (base + (int64_t)x * n_rep)]);
-        float L = 0.0f, O = 0.0f;
-        for (int x = 0; x < n_splits; x++) {
-            const int64_t pidx = base + (int64_t)x * n_rep;
-            const float mx = ws.ml[2 * pidx];
-            const float f = (mx == -INFINITY) ? 0.0f : fast_exp2(mx - M);
-            L += f * ws.ml[2 * pidx + 1];
-            O += f * ws.o[pidx * D + d];
+    int pc0 = cur.cb;  // first chunk of the current piece
+    bool first_piece = true;
+    int c = cur.cb;
+    load_q(cur.b, cur.g);
+
+    // One stream step: prefetch the chunk after c into (kn, vn) (PREFETCH is a compile-time
+    // constant at each call, so the steady-state loop has no conditional loads), compute c
+    // from (kc, vc), then advance the cursor.
+    auto step = [&](auto prefetch, u32x4 (*kc)[4], u32x4 (*vc)[4], u32x4 (*kn)[4],
+                    u32x4 (*vn)[4]) {
+        if constexpr (decltype(prefetch)::value) {
+            const bool in_cur = c + 1 < cur.ce;
+            const int pg = in_cur ? cur.g : nxt.g;
+            const int pslots = in_cur ? cur_slots : nxt_slots;
+            const int ptile = in_cur ? 2 * (c + 1 - cur.cb) : 0;
+            load_chunk(pg, pslots, ptile, kn, vn);
         }
-        out_g[idx] = from_f32<TO>(O / L);
+        compute_chunk(c, cur.tok_end, kc, vc);
+        if (c + 1 < cur.ce) {
+            c += 1;
+            return;
+        }
+        // end of a segment
+        const bool piece_end = !has_nxt || nxt.b != cur.b || nxt.g != cur.g;
+        if (piece_end) epilogue(cur.b, cur.g, pc0 == 0 && cur.ce == cur.nch, first_piece);
+        if (!has_nxt) return;
+        if (piece_end) {
+            pc0 = nxt.cb;
+            first_piece = false;
+            load_q(nxt.b, nxt.g);
+        }
+        cur = nxt;
+        cur_slots = nxt_slots;
+        c = cur.cb;
+        nx += cur.ce - cur.cb;
+        has_nxt = nx < hi;
+        if (has_nxt) {
+            nxt = seg_at(nx);
+            nxt_slots = seg_slots(nxt);
+        }
+    };
+
+    using pf_on = std::integral_constant<bool, true>;
+    using pf_off = std::integral_constant<bool, false>;
+    u32x4 ka[2][4], va[2][4], kb[2][4], vb[2][4];
+    load_chunk(cur.g, cur_slots, 0, ka, va);
+    int64_t remaining = hi - lo;  // chunks this wave computes; all but the last prefetch one
+    for (; remaining > 2; remaining -= 2) {
+        step(pf_on{}, ka, va, kb, vb);
+        step(pf_on{}, kb, vb, ka, va);
     }
-    if (tid == 0) ws.counters[unit] = 0;  // leave the counter ready for the next call
+    if (remaining == 2) {
+        step(pf_on{}, ka, va, kb, vb);
+        step(pf_off{}, kb, vb, ka, va);
+    } else {
+        step(pf_off{}, ka, va, kb, vb);
+    }
+}
+
+// Merge of the pieces of pairs cut by wave ranges, and zero rows for empty contexts: one
+// workgroup per (query head, sequence), one lane per output dim. Pieces are taken 128 at a
+// time (one per lane): their (max, sum) pairs become weights through two block reductions,
+// then every lane accumulates its dim over the batch with independent loads; batches combine
+// with the same online rescaling as the running update of cpu.rs:96-105.
+template <typename TO>
+__global__ __launch_bounds__(DEC_D) void paged_decode_merge_kernel(
+    TO* __restrict__ out, const int32_t* __restrict__ context_lens, int batch, int num_heads,
+    int kv_heads, int n_rep, int max_ctx, int nwg_i, DecodeWs ws) {
+    constexpr int D = DEC_D;
+    __shared__ float red_f[DEC_D / 64];
+    __shared__ int red_i[2][DEC_D / 64];
+    __shared__ float w_s[DEC_D];
+    __shared__ int slot_s[DEC_D];
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x, wv = d >> 6;
+    const int nch = decode_chunks(context_lens[b], max_ctx);
+    TO* o = out + ((int64_t)b * num_heads + h) * D;
+    if (nch == 0) {
+        o[d] = from_f32<TO>(0.0f);
+        return;
+    }
+    // chunks before sequence b, and in all sequences
+    int before = 0, all = 0;
+    for (int i = d; i < batch; i += D) {
+        const int n = decode_chunks(context_lens[i], max_ctx);
+        all += n;
+        if (i < b) before += n;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        before += __shfl_xor(before, off, 64);
+        all += __shfl_xor(all, off, 64);
+    }
+    if ((d & 63) == 0) {
+        red_i[0][wv] = before;
+        red_i[1][wv] = all;
+    }
+    __syncthreads();
+    before = red_i[0][0] + red_i[0][1];
+    all = red_i[1][0] + red_i[1][1];
+    const int g = h / n_rep, hh = h - g * n_rep;
+    const int64_t total = (int64_t)kv_heads * all, nwg = nwg_i;
+    const int64_t s = (int64_t)kv_heads * before + (int64_t)g * nch;
+    const int64_t e = s + nch;
+    const int64_t f = owner_wg(s, total, nwg), l = owner_wg(e - 1, total, nwg);
+    if (f == l) return;  // finished inside one wave range
+    const bool f_first = (s == f * total / nwg);
+    const int np = (int)(l - f + 1);  // ranges f..l; empty ones wrote nothing
+
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int p0 = 0; p0 < np; p0 += D) {
+        const int64_t i = f + p0 + d;
+        int slot = -1;
+        float mx = -INFINITY, lx = 0.0f;
+        if (p0 + d < np && i * total / nwg != (i + 1) * total / nwg) {
+            slot = (int)((i == f && !f_first) ? 2 * i + 1 : 2 * i);
+            mx = ws.ml[2 * ((int64_t)slot * n_rep + hh)];
+            lx = ws.ml[2 * ((int64_t)slot * n_rep + hh) + 1];
+        }
+        float bm = mx;
+        for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
+        if ((d & 63) == 0) red_f[wv] = bm;
+        __syncthreads();
+        const float m_new = fmaxf(M, fmaxf(red_f[0], red_f[1]));
+        const float w = (slot >= 0) ? fast_exp2(mx - m_new) : 0.0f;
+        w_s[d] = w;
+        slot_s[d] = slot;
+        float bl = w * lx;
+        for (int off = 32; off > 0; off >>= 1) bl += __shfl_xor(bl, off, 64);
+        __syncthreads();  // red_f reads done; w_s / slot_s visible
+        if ((d & 63) == 0) red_f[wv] = bl;
+        __syncthreads();
+        const float c_old = (M == -INFINITY) ? 0.0f : fast_exp2(M - m_new);
+        L = L * c_old + (red_f[0] + red_f[1]);
+        O *= c_old;
+        // Unconditional loads (an empty range reads a valid row of the first piece) so they
+        // are all in flight together; the select drops them, so stale workspace bits (even
+        // NaN) never reach the sum.
+        // Groups of 8 straight-line loads: entries past the batch hold slot -1 (weight 0).
+        const int nb8 = (min(D, np - p0) + 7) & ~7;
+        const int sl0 = slot_s[0] >= 0 ? slot_s[0] : slot_s[1];
+        for (int q = 0; q < nb8; q += 8) {
+            float v[8];
+            int sl[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                sl[j] = slot_s[q + j];
+                v[j] = ws.o[((int64_t)(sl[j] >= 0 ? sl[j] : sl0) * n_rep + hh) * D + d];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) O += (sl[j] >= 0) ? w_s[q + j] * v[j] : 0.0f;
+        }
+        M = m_new;
+        __syncthreads();  // w_s / slot_s / red_f are rewritten by the next batch
+    }
+    o[d] = from_f32<TO>(O / L);
 }
 
 template <typename T, typename TO>
 static int launch_decode_mfma(void* out, const void* q, const void* k_pool, const void* v_pool,
                               const int32_t* bt, int max_blocks, const int32_t* ctx_lens,
                               int batch, int num_heads, int kv_heads, int n_rep, int block_size,
-                              int64_t num_slots, int max_ctx, float scale, int split_tokens,
-                              int max_splits, DecodeWs ws, hipStream_t stream) {
-    const size_t lds = (size_t)(DEC_WAVES * n_rep * DEC_D + 2 * DEC_WAVES * n_rep) * sizeof(float);
-    dim3 grid(max_splits, kv_heads, batch);
-    paged_decode_mfma_kernel<T, TO><<<grid, dim3(DEC_THREADS), lds, stream>>>(
+                              int64_t num_slots, int max_ctx, float scale, int nwg, DecodeWs ws,
+                              hipStream_t stream) {
+    const size_t lds = (size_t)(batch + 1) * sizeof(int);
+    auto kern = block_size == 16 ? paged_decode_mfma_kernel<T, TO, true>
+                                 : paged_decode_mfma_kernel<T, TO, false>;
+    kern<<<dim3(nwg), dim3(64), lds, stream>>>(
         static_cast<TO*>(out), static_cast<const T*>(q), static_cast<const T*>(k_pool),
-        static_cast<const T*>(v_pool), bt, max_blocks, ctx_lens, num_heads, kv_heads, n_rep,
-        block_size, num_slots, max_ctx, scale * LOG2E, split_tokens, max_splits, ws);
-    return check_hip(hipGetLastError(), "paged_decode launch");
+        static_cast<const T*>(v_pool), bt, max_blocks, ctx_lens, batch, num_heads, kv_heads, n_rep,
+        block_size, num_slots, max_ctx, scale * LOG2E, ws);
+    int rc = check_hip(hipGetLastError(), "paged_decode launch");
+    if (rc != FLOUR_OK) return rc;
+    paged_decode_merge_kernel<TO><<<dim3(num_heads, batch), dim3(DEC_D), 0, stream>>>(
+        static_cast<TO*>(out), ctx_lens, batch, num_heads, kv_heads, n_rep, max_ctx, nwg, ws);
+    return check_hip(hipGetLastError(), "paged_decode merge launch");
 }
 
 }  // namespace flour
 
 using namespace flour;
+
+extern "C" int flour_hip_set_decode_workgroups(int n) {
+    if (n < 0 || n > 4096) return FLOUR_ERR_INVALID_ARGUMENT;
+    g_wg_override = n;
+    return FLOUR_OK;
+}
 
 extern "C" int flour_hip_paged_decode_workspace_size(int batch, int num_heads, int kv_heads,
                                                      int head_dim, int max_context_len,
@@ -312,9 +559,7 @@ extern "C" int flour_hip_paged_decode_workspace_size(int batch, int num_heads, i
         set_error("paged_decode_workspace_size: bad arguments");
         return FLOUR_ERR_INVALID_ARGUMENT;
     }
-    const int split = choose_split_tokens(batch, kv_heads, max_context_len);
-    const int max_splits = max_context_len > 0 ? (max_context_len + split - 1) / split : 1;
-    *bytes = decode_ws_bytes(batch, kv_heads, num_heads / kv_heads, head_dim, max_splits);
+    *bytes = decode_ws_bytes(decode_workgroups(), num_heads / kv_heads, head_dim);
     return FLOUR_OK;
 }
 
@@ -332,12 +577,13 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
         return FLOUR_ERR_INVALID_ARGUMENT;
     }
     if (batch < 0 || num_heads <= 0 || kv_heads <= 0 || num_heads % kv_heads != 0 ||
-        head_dim <= 0 || block_size <= 0 || num_slots <= 0 || max_blocks_per_seq <= 0 ||
-        max_context_len < 0 || (int64_t)max_context_len > (int64_t)max_blocks_per_seq * block_size) {
+        head_dim <= 0 || block_size <= 0 || num_slots <= 0 || num_slots % block_size != 0 ||
+        max_blocks_per_seq <= 0 || max_context_len < 0 ||
+        (int64_t)max_context_len > (int64_t)max_blocks_per_seq * block_size) {
         set_error("paged_decode: bad shape (batch=%d heads=%d kv_heads=%d head_dim=%d bs=%d "
-                  "max_blocks=%d max_ctx=%d)",
-                  batch, num_heads, kv_heads, head_dim, block_size, max_blocks_per_seq,
-                  max_context_len);
+                  "num_slots=%lld max_blocks=%d max_ctx=%d)",
+                  batch, num_heads, kv_heads, head_dim, block_size, (long long)num_slots,
+                  max_blocks_per_seq, max_context_len);
         return FLOUR_ERR_INVALID_ARGUMENT;
     }
     if (batch == 0) return FLOUR_OK;
@@ -349,6 +595,8 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
     const int n_rep = num_heads / kv_heads;
     const bool mfma = (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
                       head_dim == DEC_D && block_size % 16 == 0 && n_rep <= 16 &&
+                      batch <= DEC_MAX_BATCH && num_heads <= 65535 &&
+                      num_slots * head_dim * 2 <= (int64_t)0x7fffffff &&
                       ((uintptr_t)q % 16 == 0) && ((uintptr_t)k_pool % 16 == 0) &&
                       ((uintptr_t)v_pool % 16 == 0);
     if (!mfma) {
@@ -359,45 +607,35 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
                                    batch, num_heads, n_rep, head_dim, block_size, num_slots, scale,
                                    s);
     }
-    if (batch > 65535 || kv_heads > 65535) {
-        set_error("paged_decode: batch/kv_heads beyond grid limits");
-        return FLOUR_ERR_UNSUPPORTED;
+    const int nwg = decode_workgroups();
+    const size_t need = decode_ws_bytes(nwg, n_rep, head_dim);
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 256) != 0) {
+        set_error("paged_decode: workspace of %zu bytes (256-byte aligned) required, got %zu "
+                  "at %p",
+                  need, workspace_bytes, workspace);
+        return FLOUR_ERR_WORKSPACE;
     }
-    const int split = choose_split_tokens(batch, kv_heads, max_context_len);
-    const int max_splits = max_context_len > 0 ? (max_context_len + split - 1) / split : 1;
-    DecodeWs ws{nullptr, nullptr, nullptr};
-    if (max_splits > 1) {
-        const size_t need = decode_ws_bytes(batch, kv_heads, n_rep, head_dim, max_splits);
-        if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 256) != 0) {
-            set_error("paged_decode: workspace of %zu bytes (256-byte aligned, zero-filled once) "
-                      "required, got %zu at %p",
-                      need, workspace_bytes, workspace);
-            return FLOUR_ERR_WORKSPACE;
-        }
-        const size_t units = (size_t)batch * kv_heads;
-        char* p = static_cast<char*>(workspace);
-        ws.counters = reinterpret_cast<int*>(p);
-        p += align256(units * sizeof(int));
-        ws.ml = reinterpret_cast<float*>(p);
-        p += align256(units * max_splits * n_rep * 2 * sizeof(float));
-        ws.o = reinterpret_cast<float*>(p);
-    }
+    DecodeWs ws;
+    ws.ml = static_cast<float*>(workspace);
+    ws.o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                    align256((size_t)2 * nwg * n_rep * 2 * sizeof(float)));
 #define FLOUR_DEC(T)                                                                            \
     do {                                                                                        \
         if (out_dtype == FLOUR_DTYPE_F32)                                                       \
             return launch_decode_mfma<T, float>(out, q, k_pool, v_pool, block_tables,           \
                                                 max_blocks_per_seq, context_lens, batch,        \
                                                 num_heads, kv_heads, n_rep, block_size,         \
-                                                num_slots, max_context_len, scale, split, max_splits, ws, s);    \
+                                                num_slots, max_context_len, scale, nwg, ws, s); \
         if (out_dtype == FLOUR_DTYPE_BF16)                                                      \
             return launch_decode_mfma<T, bf16_t>(out, q, k_pool, v_pool, block_tables,          \
                                                  max_blocks_per_seq, context_lens, batch,       \
                                                  num_heads, kv_heads, n_rep, block_size,        \
-                                                 num_slots, max_context_len, scale, split, max_splits, ws, s);   \
+                                                 num_slots, max_context_len, scale, nwg, ws,    \
+                                                 s);                                            \
         return launch_decode_mfma<T, f16_t>(out, q, k_pool, v_pool, block_tables,               \
                                             max_blocks_per_seq, context_lens, batch, num_heads, \
                                             kv_heads, n_rep, block_size, num_slots,             \
-                                            max_context_len, scale, split, max_splits, ws, s);                          \
+                                            max_context_len, scale, nwg, ws, s);                \
     } while (0)
     if (dtype == FLOUR_DTYPE_BF16) FLOUR_DEC(bf16_t);
     FLOUR_DEC(f16_t);

@@ -84,10 +84,9 @@ def decode_workspace_bytes(batch: int, num_heads: int, kv_heads: int, head_dim: 
 
 
 class DecodeWorkspace:
-    """Zero-filled device scratch for split-context decode; grows on demand and is reused.
+    """Device scratch for split-context decode partials; grows on demand and is reused.
 
-    The kernels leave its counters at zero after every call, so it is cleared only when it is
-    (re)allocated. Calls sharing one workspace must not overlap in time.
+    Calls sharing one workspace must not overlap in time (one stream, or explicit ordering).
     """
 
     def __init__(self, device: torch.device | str = "cuda"):
@@ -96,7 +95,7 @@ class DecodeWorkspace:
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self.buf
 
 

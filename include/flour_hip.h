@@ -86,11 +86,10 @@ int flour_hip_kv_write(const void* k, const void* v, int64_t stride_tok, int64_t
  *   scale multiplies q.k before the softmax (attention.rs:108 passes 1/sqrt(head_dim)).
  *   max_context_len bounds context_lens[] and sizes the split-context grid.
  *
- * Long contexts are split across workgroups; partial (max, sum, acc) rows are merged by the
- * last workgroup of each (sequence, kv head). `workspace` holds those partials plus one
- * counter per (sequence, kv head): it must be zero-filled once when first allocated, and
- * every call leaves the counters at zero again. Calls that share a workspace must not
- * overlap in time. flour_hip_paged_decode_workspace_size gives the bytes required.
+ * Long contexts are split across workgroups; partial (max, sum, acc) rows go to `workspace`
+ * (device memory, 256-byte aligned, no initialisation needed) and a second kernel on the same
+ * stream merges them. flour_hip_paged_decode_workspace_size gives the bytes required; calls
+ * that share a workspace must not overlap in time.
  * ---------------------------------------------------------------------------------------- */
 int flour_hip_paged_decode_workspace_size(int batch, int num_heads, int kv_heads, int head_dim,
                                           int max_context_len, size_t* bytes);
