@@ -156,6 +156,17 @@ __device__ __forceinline__ uint32_t perm_hi16(uint32_t lo_src, uint32_t hi_src) 
     return __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);
 }
 
+// IEEE maximum (NaN-propagating): lowers to v_maximum3_f32 chains with no canonicalising moves,
+// unlike fmaxf, whose NaN-quieting rule costs one extra instruction per MFMA-produced operand.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// max(x, x of lane l^32): one row-swap (VALU) instead of an LDS permute.
+__device__ __forceinline__ float max_across_halves(float x) {
+    const uint32_t u = __float_as_uint(x);
+    auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ float wave_shfl_xor(float x, int mask) {
     return __shfl_xor(x, mask, 64);
 }

@@ -30,6 +30,8 @@
 //    mantissa bits of the softmax weights; otherwise P is rounded once to 16 bits.
 #include <math.h>
 
+#include <type_traits>
+
 #include "flour_common.h"
 
 namespace flour {
@@ -42,9 +44,11 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
                         float scale, hipStream_t stream);
 
 static constexpr int PF_D = 128;
-static constexpr int PF_QT = 128;  // query rows per workgroup
+static constexpr int PF_QT = 128;  // query rows per head per workgroup (4 waves x 32)
 static constexpr int PF_KT = 64;   // kv tokens per tile
-static constexpr int PF_THREADS = 256;
+static constexpr int PF_WAVES = 8; // two query heads of one kv head x 4 waves
+static constexpr int PF_THREADS = PF_WAVES * 64;
+static constexpr float PF_RESCALE_SLACK = 8.0f;  // log2 units the reference max may lag
 static constexpr int PF_KPITCH = PF_D + 8;   // elements: 272 B rows
 static constexpr int PF_VPITCH = PF_KT + 8;  // elements: 144 B rows
 static constexpr float PF_LOG2E = 1.4426950408889634f;
@@ -53,26 +57,47 @@ __device__ __forceinline__ int swap_bits01(int x) {
     return (x & ~3) | ((x & 1) << 1) | ((x >> 1) & 1);
 }
 
-template <typename T, typename TO, bool PRECISE_P>
-__global__ __launch_bounds__(PF_THREADS, 2) void varlen_prefill_mfma_kernel(
+// P.V arithmetic of the MFMA path.
+//  PV_F16:   P rounded once to fp16 (11 significant bits; P is in [0, 1]) and V widened
+//            exactly to fp16 when the pool is bf16 (exact for |v| < 65504, the fp16 range);
+//            one MFMA per product.
+//  PV_HILO:  P split into hi + lo parts of the storage type (~16 significant bits), V in the
+//            storage type; two MFMAs per product.
+enum { PV_F16 = 0, PV_HILO = 1 };
+
+static constexpr uint32_t PF_OOR = 0x80000000u;  // buffer offset past any pool: loads read 0
+
+__device__ __forceinline__ int sigma16(int t) {  // swap bits 2 and 3 (token order in V^T rows)
+    return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1);
+}
+
+template <typename T, typename TO, int PV, bool BS16>
+__global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     TO* __restrict__ out, int64_t o_st, int64_t o_sh, const T* __restrict__ q, int64_t q_st,
     int64_t q_sh, const T* __restrict__ k_pool, const T* __restrict__ v_pool,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ block_tables, int max_blocks, int num_seqs, int num_heads,
     int n_rep, int block_size, int64_t num_slots, float scale_log2) {
     constexpr int D = PF_D;
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[PF_KT * PF_KPITCH];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[PF_D * PF_VPITCH];
+    // V^T is staged as fp16 for PV_F16, as the storage type otherwise; K keeps the storage type.
+    typedef typename std::conditional<PV == PV_F16, f16_t, T>::type TV;
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][PF_KT * PF_KPITCH];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][PF_D * PF_VPITCH];
 
-    // ---- work item: (query tile from the end, sequence, head)
-    const int per_rank = num_seqs * num_heads;
+    // ---- work item: (query tile from the end, sequence, pair of query heads)
+    const int pairs_per_kv = (n_rep + 1) >> 1;
+    const int kv_heads = num_heads / n_rep;
+    const int per_rank = num_seqs * kv_heads * pairs_per_kv;
     const int bid = blockIdx.x;
     const int tile_rev = bid / per_rank;
     int r = bid - tile_rev * per_rank;
     const int full8 = per_rank & ~7;
     if (r < full8) r = (r & 7) * (full8 >> 3) + (r >> 3);
-    const int seq = r / num_heads;
-    const int head = r - seq * num_heads;
+    const int npairs = kv_heads * pairs_per_kv;
+    const int seq = r / npairs;
+    const int hp = r - seq * npairs;
+    const int kvh = hp / pairs_per_kv;
+    const int hj = hp - kvh * pairs_per_kv;
 
     const int q0 = cu_seqlens[seq];
     const int ql = cu_seqlens[seq + 1] - q0;
@@ -92,81 +117,101 @@ __global__ __launch_bounds__(PF_THREADS, 2) void varlen_prefill_mfma_kernel(
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int h2 = lane >> 5, ql32 = lane & 31;
-    const int kvh = head / n_rep;
+    const int hsel = w >> 2;  // which head of the pair
+    const int head = kvh * n_rep + 2 * hj + hsel;
+    const bool head_ok = 2 * hj + hsel < n_rep;
     const int32_t* bt = block_tables + (int64_t)seq * max_blocks;
-    const T* k_head = k_pool + (int64_t)kvh * num_slots * D;
-    const T* v_head = v_pool + (int64_t)kvh * num_slots * D;
     const int64_t max_phys = num_slots / block_size - 1;
+    const int last_page = (kv_len - 1) / block_size;
+    const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(k_pool + (int64_t)kvh * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(v_pool + (int64_t)kvh * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
 
     // ---- this lane's query row and its causal limit (padded rows copy the last valid row)
-    const int wr0 = row_begin + 32 * w;
-    const bool wave_active = wr0 < ql;
+    const int wr0 = row_begin + 32 * (w & 3);
+    const bool wave_active = head_ok && wr0 < ql;
     const int qrow = min(wr0 + ql32, ql - 1);
-    const int lim = off + qrow;                       // visible kv j <= lim
+    const int lim = off + qrow;                        // visible kv j <= lim
     const int wave_lim = off + min(wr0 + 31, ql - 1);  // largest limit in the wave
     const int wave_min_lim = off + wr0;                // smallest limit in the wave
 
     // Q^T as the B operand: lane (h2, q) holds row q, dims 16kk + 8h2 .. +7.
     u32x4 qb[8];
     {
-        const T* qp = q + (int64_t)(q0 + qrow) * q_st + (int64_t)head * q_sh + 8 * h2;
+        const int hq = head_ok ? head : head - 1;  // idle waves read a valid row
+        const T* qp = q + (int64_t)(q0 + qrow) * q_st + (int64_t)hq * q_sh + 8 * h2;
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) qb[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
     }
 
-    // ---- staging assignment
-    // K: 4 chunks of 16 B per thread: chunk c = tid + 256 i -> token c / 16, dims (c % 16) * 8.
-    // V: token quad tq = tid % 16 (tokens 4tq..4tq+3), dims 8 dg .. 8 dg + 7 with dg = tid / 16.
-    const int v_tq = tid & 15, v_dg = tid >> 4;
-    u32x4 kst[4], vst[4];
-    auto slot_of = [&](int tok) -> int64_t {
-        const int lb = tok / block_size;
-        int64_t phys = bt[lb];
-        phys = phys < 0 ? 0 : (phys > max_phys ? max_phys : phys);
-        return phys * block_size + (tok - lb * block_size);
+    // ---- staging assignment (a 64-token tile is four 16-token groups, each inside one page)
+    // K: two 16 B chunks per thread: token (tid / 16) + 32i of the tile, dims (tid % 16) * 8.
+    // V: token pair tp = tid % 32 (tokens 2tp, 2tp+1), dims 8dg..8dg+7 with dg = tid / 32;
+    //    stored transposed, token t at column sigma16(t).
+    const int k_row = tid >> 4, k_col = (tid & 15) * 8;
+    const int v_tp = tid & 31, v_dg = tid >> 5;
+    // Pool slot of the first token of each group of a tile: workgroup-uniform, read through
+    // the scalar cache.
+    auto page_bases = [&](int kt, int* pb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tok0 = kt * PF_KT + 16 * i;
+            const int lb = min(BS16 ? (tok0 >> 4) : tok0 / block_size, last_page);
+            int64_t phys = bt[lb];  // clamped: a bad block id never leaves the pool
+            phys = phys < 0 ? 0 : (phys > max_phys ? max_phys : phys);
+            pb[i] = (int)(phys * block_size + (tok0 - lb * block_size));
+        }
     };
-    auto gload = [&](int kt) {
+    // Branch-free tile loads into (kd, vd): tokens past kv_len (or a tile past the last) get an
+    // out-of-range offset and read zeros.
+    auto gload = [&](int kt, const int* pb, bool valid, u32x4* kd, u32x4* vd) {
         const int kv0 = kt * PF_KT;
+        const int lim_tok = valid ? kv_len : 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + PF_THREADS * i;
-            const int tok = kv0 + (c >> 4);
-            if (tok < kv_len)
-                kst[i] = *reinterpret_cast<const u32x4*>(k_head + slot_of(tok) * D + (c & 15) * 8);
-            else
-                kst[i] = u32x4{0, 0, 0, 0};
+        for (int i = 0; i < 2; i++) {
+            const int t = k_row + 32 * i;
+            const int g = t >> 4;
+            const int base = g == 0 ? pb[0] : g == 1 ? pb[1] : g == 2 ? pb[2] : pb[3];
+            const uint32_t o = (uint32_t)((base + (t & 15)) * D + k_col) * (uint32_t)sizeof(T);
+            kd[i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, kv0 + t < lim_tok ? o : PF_OOR,
+                                                          0, 0);
         }
+        const int g = v_tp >> 3;
+        const int base = g == 0 ? pb[0] : g == 1 ? pb[1] : g == 2 ? pb[2] : pb[3];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int tok = kv0 + 4 * v_tq + j;
-            if (tok < kv_len)
-                vst[j] = *reinterpret_cast<const u32x4*>(v_head + slot_of(tok) * D + 8 * v_dg);
-            else
-                vst[j] = u32x4{0, 0, 0, 0};
+        for (int j = 0; j < 2; j++) {
+            const int t = 2 * v_tp + j;
+            const uint32_t o =
+                (uint32_t)((base + (t & 15)) * D + 8 * v_dg) * (uint32_t)sizeof(T);
+            vd[j] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, kv0 + t < lim_tok ? o : PF_OOR,
+                                                          0, BUF_NT);
         }
     };
-    auto lds_store = [&]() {
+    auto lds_store = [&](int buf, u32x4* kd, u32x4* vd) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + PF_THREADS * i;
-            *reinterpret_cast<u32x4*>(&Ks[(c >> 4) * PF_KPITCH + (c & 15) * 8]) = kst[i];
+        for (int i = 0; i < 2; i++)
+            *reinterpret_cast<u32x4*>(&Ks[buf][(k_row + 32 * i) * PF_KPITCH + k_col]) = kd[i];
+        if constexpr (PV == PV_F16 && std::is_same<T, bf16_t>::value) {
+            // widen bf16 V to fp16 (exact inside the fp16 range)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int x = 0; x < 4; x++)
+                    vd[j][x] = pack2<f16_t>(lo_f32<bf16_t>(vd[j][x]), hi_f32<bf16_t>(vd[j][x]));
         }
-        const int col = 4 * swap_bits01(v_tq);
+        const int col = sigma16(2 * v_tp);  // the pair stays adjacent under sigma16
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int wd = e >> 1;
-            u32x2 pr;
-            if (e & 1) {
-                pr[0] = perm_hi16(vst[0][wd], vst[1][wd]);
-                pr[1] = perm_hi16(vst[2][wd], vst[3][wd]);
-            } else {
-                pr[0] = perm_lo16(vst[0][wd], vst[1][wd]);
-                pr[1] = perm_lo16(vst[2][wd], vst[3][wd]);
-            }
-            *reinterpret_cast<u32x2*>(&Vt[(8 * v_dg + e) * PF_VPITCH + col]) = pr;
+            const uint32_t pr = (e & 1) ? perm_hi16(vd[0][wd], vd[1][wd]) : perm_lo16(vd[0][wd], vd[1][wd]);
+            *reinterpret_cast<uint32_t*>(&Vt[buf][(8 * v_dg + e) * PF_VPITCH + col]) = pr;
         }
     };
 
+    // Running state: the reference max m may lag the true running max by up to
+    // PF_RESCALE_SLACK (weights then reach 2^8), which skips most accumulator rescales.
     float m = -INFINITY, lsum = 0.0f;
     f32x16 o[4];
 #pragma unroll
@@ -174,87 +219,118 @@ __global__ __launch_bounds__(PF_THREADS, 2) void varlen_prefill_mfma_kernel(
 #pragma unroll
         for (int y = 0; y < 16; y++) o[x][y] = 0.0f;
 
-    gload(0);
-    for (int kt = 0; kt < n_kt; kt++) {
-        lds_store();
-        __syncthreads();
-        if (kt + 1 < n_kt) gload(kt + 1);
-
+    auto compute = [&](int kt, int buf) {
         const int kv0 = kt * PF_KT;
-        if (wave_active && kv0 <= wave_lim) {
-            // ---- S^T tile (64 tokens x 32 queries) in two 32-token halves
-            f32x16 st[2];
+        if (!(wave_active && kv0 <= wave_lim)) return;  // uniform per wave
+        // ---- S^T tile (64 tokens x 32 queries) in two 32-token halves, raw q.k
+        f32x16 st[2];
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
+        for (int mt = 0; mt < 2; mt++) {
 #pragma unroll
-                for (int y = 0; y < 16; y++) st[mt][y] = 0.0f;
-                const uint16_t* kr = &Ks[(32 * mt + ql32) * PF_KPITCH + 8 * h2];
+            for (int y = 0; y < 16; y++) st[mt][y] = 0.0f;
+            const uint16_t* kr = &Ks[buf][(32 * mt + ql32) * PF_KPITCH + 8 * h2];
 #pragma unroll
-                for (int kk = 0; kk < 8; kk++) {
-                    const u32x4 a = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
-                    st[mt] = mfma32x32x16<T>(a, qb[kk], st[mt]);
-                }
+            for (int kk = 0; kk < 8; kk++) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
+                st[mt] = mfma32x32x16<T>(a, qb[kk], st[mt]);
             }
-            // ---- scale, mask, running max
-            const bool need_mask = kv0 + PF_KT - 1 > wave_min_lim;
+        }
+        // ---- mask, on tiles that cross the diagonal of some row of this wave only. The empty
+        // asm statements keep the compiler from if-converting these uniform branches into
+        // per-element selects on every tile.
+        if (kv0 + PF_KT - 1 > wave_min_lim) {
+            asm volatile("" ::: "memory");
             const int tl = lim - kv0 - 4 * h2;  // token offset 32mt + 8i + j visible iff <= tl
-            float tmax = -INFINITY;
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        float v = st[mt][4 * i + j] * scale_log2;
-                        if (need_mask && (32 * mt + 8 * i + j > tl)) v = -INFINITY;
-                        st[mt][4 * i + j] = v;
-                        tmax = fmaxf(tmax, v);
-                    }
-            tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
+                    for (int j = 0; j < 4; j++)
+                        if (32 * mt + 8 * i + j > tl) st[mt][4 * i + j] = -INFINITY;
+        }
+        // ---- tile max of the raw scores (scale > 0, so the max commutes with the scaling)
+        float tm[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int y = 0; y < 16; y += 2) tm[mt] = vmax(vmax(tm[mt], st[mt][y]), st[mt][y + 1]);
+        const float tmax = max_across_halves(vmax(tm[0], tm[1])) * scale_log2;
+        if (__builtin_amdgcn_ballot_w64(tmax > m + PF_RESCALE_SLACK) != 0) {
+            asm volatile("" ::: "memory");
             const float m_new = fmaxf(m, tmax);
             const float alpha = fast_exp2(m - m_new);
-            float psum = 0.0f;
+            lsum *= alpha;
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int y = 0; y < 16; y++) {
-                    const float p = fast_exp2(st[mt][y] - m_new);
-                    st[mt][y] = p;
-                    psum += p;
-                }
-            lsum = lsum * alpha + psum;
-            if (__builtin_amdgcn_ballot_w64(m_new > m) != 0) {
-#pragma unroll
-                for (int x = 0; x < 4; x++) o[x] *= alpha;
-            }
+            for (int x = 0; x < 4; x++) o[x] *= alpha;
             m = m_new;
-
-            // ---- P^T B operands: kk2 covers tokens of half kk2/2, rows i = 2(kk2&1), +1
-            u32x4 pb[4], pl[4];
+        }
+        // ---- p = 2^(s * scale_log2 - m), one FMA + exp per score, then the P^T B operands:
+        // kk2 covers tokens of half kk2/2, rows i = 2(kk2&1), +1. The row sum is taken over the
+        // rounded weights that enter the product (v_dot2 over fp16 pairs) in PV_F16 mode.
+        const float nm = -m;
+        u32x4 pb_hi[4], pb_lo[4];
+        float psum = 0.0f;
 #pragma unroll
-            for (int kk2 = 0; kk2 < 4; kk2++) {
-                const int mt = kk2 >> 1, y0 = 8 * (kk2 & 1);
+        for (int kk2 = 0; kk2 < 4; kk2++) {
+            const int mt = kk2 >> 1, y0 = 8 * (kk2 & 1);
 #pragma unroll
-                for (int x = 0; x < 4; x++) {
-                    const float a0 = st[mt][y0 + 2 * x], a1 = st[mt][y0 + 2 * x + 1];
-                    const uint32_t hi = pack2<T>(a0, a1);
-                    pb[kk2][x] = hi;
-                    if (PRECISE_P) pl[kk2][x] = pack2<T>(a0 - lo_f32<T>(hi), a1 - hi_f32<T>(hi));
-                }
-            }
-            // ---- O^T += V^T P^T
-#pragma unroll
-            for (int mt2 = 0; mt2 < 4; mt2++) {
-                const uint16_t* vr = &Vt[(32 * mt2 + ql32) * PF_VPITCH + 8 * h2];
-#pragma unroll
-                for (int kk2 = 0; kk2 < 4; kk2++) {
-                    const u32x4 a = *reinterpret_cast<const u32x4*>(vr + 16 * kk2);
-                    o[mt2] = mfma32x32x16<T>(a, pb[kk2], o[mt2]);
-                    if (PRECISE_P) o[mt2] = mfma32x32x16<T>(a, pl[kk2], o[mt2]);
+            for (int x = 0; x < 4; x++) {
+                const float a0 = fast_exp2(fmaf(st[mt][y0 + 2 * x], scale_log2, nm));
+                const float a1 = fast_exp2(fmaf(st[mt][y0 + 2 * x + 1], scale_log2, nm));
+                const uint32_t hi = pack2<TV>(a0, a1);
+                pb_hi[kk2][x] = hi;
+                if constexpr (PV == PV_HILO) {
+                    pb_lo[kk2][x] = pack2<TV>(a0 - lo_f32<TV>(hi), a1 - hi_f32<TV>(hi));
+                    psum += a0 + a1;
+                } else {
+                    psum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, hi), f16x2{1, 1}, psum,
+                                                  false);
                 }
             }
         }
+        lsum += psum;
+        // ---- O^T += V^T P^T
+#pragma unroll
+        for (int mt2 = 0; mt2 < 4; mt2++) {
+            const uint16_t* vr = &Vt[buf][(32 * mt2 + ql32) * PF_VPITCH + 8 * h2];
+#pragma unroll
+            for (int kk2 = 0; kk2 < 4; kk2++) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(vr + 16 * kk2);
+                o[mt2] = mfma32x32x16<TV>(a, pb_hi[kk2], o[mt2]);
+                if constexpr (PV == PV_HILO) o[mt2] = mfma32x32x16<TV>(a, pb_lo[kk2], o[mt2]);
+            }
+        }
+    };
+
+    // ---- pipeline: one barrier per tile; global loads run two tiles ahead of the compute
+    // (register sets A / B alternate), LDS double-buffered, page ids three tiles ahead.
+    u32x4 ka[2], va[2], kb[2], vb[2];
+    int pb0[4], pb1[4], pb2[4];
+    page_bases(0, pb0);
+    gload(0, pb0, true, ka, va);
+    page_bases(min(1, n_kt - 1), pb1);
+    gload(1, pb1, 1 < n_kt, kb, vb);
+    page_bases(min(2, n_kt - 1), pb2);
+    lds_store(0, ka, va);
+    __syncthreads();
+    // step kt: refill `nx` with tile kt + 2, compute tile kt, store tile kt + 1 (held in `st1`)
+    auto step = [&](int kt, u32x4* knx, u32x4* vnx, u32x4* kst1, u32x4* vst1) {
+        gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
+        page_bases(min(kt + 3, n_kt - 1), pb0);
+        compute(kt, kt & 1);
+        lds_store((kt + 1) & 1, kst1, vst1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // pb2 <- tile kt + 3
+            const int t = pb2[i];
+            pb2[i] = pb0[i];
+            pb0[i] = t;
+        }
         __syncthreads();
+    };
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, ka, va, kb, vb);
+        if (kt + 1 < n_kt) step(kt + 1, kb, vb, ka, va);
     }
 
     // ---- epilogue: lane (h2, q) holds dims 32 mt2 + 8 i + 4 h2 + j of query row wr0 + q
@@ -278,7 +354,7 @@ __global__ __launch_bounds__(PF_THREADS, 2) void varlen_prefill_mfma_kernel(
         }
 }
 
-template <typename T, typename TO, bool PRECISE>
+template <typename T, typename TO, int PV>
 static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void* q,
                                int64_t q_st, int64_t q_sh, const void* k_pool, const void* v_pool,
                                const int32_t* cu, const int32_t* kv_lens, const int32_t* bt,
@@ -286,28 +362,30 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
                                int n_rep, int block_size, int64_t num_slots, float scale,
                                hipStream_t stream) {
     const int64_t n_qt = (max_seqlen_q + PF_QT - 1) / PF_QT;
-    const int64_t grid = n_qt * num_seqs * num_heads;
+    const int64_t grid = n_qt * num_seqs * (num_heads / n_rep) * ((n_rep + 1) / 2);
     if (grid > 0x7fffffff) {
         set_error("varlen_prefill: grid too large");
         return FLOUR_ERR_UNSUPPORTED;
     }
     if (grid == 0) return FLOUR_OK;
-    varlen_prefill_mfma_kernel<T, TO, PRECISE><<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
+    auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true>
+                                 : varlen_prefill_mfma_kernel<T, TO, PV, false>;
+    kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
         static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
         static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt, max_blocks,
         num_seqs, num_heads, n_rep, block_size, num_slots, scale * PF_LOG2E);
     return check_hip(hipGetLastError(), "varlen_prefill launch");
 }
 
-// Precision mode of the P.V product on the MFMA path (1 = hi + lo split, 0 = single rounding).
-static int g_prefill_precise = 1;
+// P.V mode of the MFMA path (PV_F16 or PV_HILO); a test / tuning switch.
+static int g_prefill_pv_mode = PV_F16;
 
 }  // namespace flour
 
 using namespace flour;
 
 extern "C" int flour_hip_set_prefill_precise_p(int on) {
-    g_prefill_precise = on ? 1 : 0;
+    g_prefill_pv_mode = on ? PV_HILO : PV_F16;
     return FLOUR_OK;
 }
 
@@ -348,7 +426,9 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
                          ((q_stride_head * es) % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
                          ((o_stride_tok * oes) % 16 == 0) && ((o_stride_head * oes) % 16 == 0);
     const bool mfma = (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
-                      head_dim == PF_D && block_size % 16 == 0 && aligned;
+                      head_dim == PF_D && block_size % 16 == 0 && aligned &&
+                      num_slots % block_size == 0 && scale > 0.0f &&
+                      num_slots * head_dim * 2 <= (int64_t)0x7fffffff;
     if (!mfma) {
         return launch_attn_generic(dtype, out_dtype, out, o_stride_tok, o_stride_head, q,
                                    q_stride_tok, q_stride_head, k_pool, v_pool, cu_seqlens_q,
@@ -356,19 +436,19 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
                                    num_heads, n_rep, head_dim, block_size, num_slots, scale, s);
     }
 #define FLOUR_PF(T, TO)                                                                          \
-    return g_prefill_precise                                                                     \
-               ? launch_prefill_mfma<T, TO, true>(out, o_stride_tok, o_stride_head, q,           \
-                                                  q_stride_tok, q_stride_head, k_pool, v_pool,   \
-                                                  cu_seqlens_q, kv_lens, block_tables,           \
-                                                  max_blocks_per_seq, num_seqs, max_seqlen_q,    \
-                                                  num_heads, n_rep, block_size, num_slots,       \
-                                                  scale, s)                                      \
-               : launch_prefill_mfma<T, TO, false>(out, o_stride_tok, o_stride_head, q,          \
-                                                   q_stride_tok, q_stride_head, k_pool, v_pool,  \
-                                                   cu_seqlens_q, kv_lens, block_tables,          \
-                                                   max_blocks_per_seq, num_seqs, max_seqlen_q,   \
-                                                   num_heads, n_rep, block_size, num_slots,      \
-                                                   scale, s)
+    return g_prefill_pv_mode == PV_HILO                                                          \
+               ? launch_prefill_mfma<T, TO, PV_HILO>(out, o_stride_tok, o_stride_head, q,        \
+                                                     q_stride_tok, q_stride_head, k_pool, v_pool, \
+                                                     cu_seqlens_q, kv_lens, block_tables,        \
+                                                     max_blocks_per_seq, num_seqs, max_seqlen_q, \
+                                                     num_heads, n_rep, block_size, num_slots,    \
+                                                     scale, s)                                   \
+               : launch_prefill_mfma<T, TO, PV_F16>(out, o_stride_tok, o_stride_head, q,         \
+                                                    q_stride_tok, q_stride_head, k_pool, v_pool,  \
+                                                    cu_seqlens_q, kv_lens, block_tables,         \
+                                                    max_blocks_per_seq, num_seqs, max_seqlen_q,  \
+                                                    num_heads, n_rep, block_size, num_slots,     \
+                                                    scale, s)
     if (dtype == FLOUR_DTYPE_BF16) {
         if (out_dtype == FLOUR_DTYPE_F32) FLOUR_PF(bf16_t, float);
         if (out_dtype == FLOUR_DTYPE_BF16) FLOUR_PF(bf16_t, bf16_t);

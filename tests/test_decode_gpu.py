@@ -5,10 +5,9 @@ Tolerances (written here, per the path's contract):
   * fp32 pools:                      max-abs <= 1e-5 against the fp32 oracle;
   * bf16 pools, fp32 output:         max-abs <= 2e-3 and rel-L2 <= 1e-3 against the fp32
                                      oracle (the kernel's fp32 accumulator, before rounding);
-  * bf16 pools, bf16 output:         exactly RNE(kernel fp32 result), and within 1 bf16 ulp of
-                                     RNE(fp32 oracle) where |ref| >= 2^-10 (1e-5 abs. below)
-                                     (rounding an exact result to bf16 alone already costs
-                                     rel-L2 ~1.6e-3, so the fp32 limits cannot apply to it).
+  * bf16 pools, bf16 output:         exactly RNE(kernel fp32 result); rel-L2 within 5% of the
+                                     floor set by rounding the exact result to bf16 (~1.5e-3,
+                                     above the fp32 limit), max-abs within floor + 2e-3.
 """
 from __future__ import annotations
 

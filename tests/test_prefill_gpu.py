@@ -3,8 +3,9 @@ restatement of paged_attention (src/backend/cpu.rs:57-112) for seq_q >= 1, inclu
 over prefix-cached shared blocks, on identical seeded inputs.
 
 Tolerances: fp32 pools max-abs <= 1e-5; bf16 pools with fp32 output max-abs <= 2e-3 and
-rel-L2 <= 1e-3 against the fp32 oracle; bf16 output exactly RNE(kernel fp32 result) and
-within 1 bf16 ulp of RNE(fp32 oracle) where |ref| >= 2^-10 (1e-5 absolute below).
+rel-L2 <= 1e-3 against the fp32 oracle; bf16 output exactly RNE(kernel fp32 result), its
+rel-L2 within 5% of the floor set by rounding the exact result to bf16 (~1.5e-3), max-abs
+within that floor + 2e-3.
 """
 from __future__ import annotations
 
@@ -133,18 +134,19 @@ def test_prefill_reference_layout_and_strided_output(device):
     assert torch.equal(out_ref.transpose(0, 1), packed)
 
 
-def test_prefill_single_rounding_mode_still_within_bf16_output_bound(device):
-    """The optional single-rounding P mode (faster) keeps bf16 outputs within 1 ulp."""
+def test_prefill_hilo_mode_meets_the_same_bounds(device):
+    """The alternative P.V mode (P split into bf16 hi + lo parts, two MFMAs per product)
+    meets the same fp32-accumulator bounds as the default fp16 P.V."""
     from flour_amd import _lib
     c = make_prefill(3, 32, 8, 128, 16, (1, 1), dtype=torch.bfloat16, seed=5, device=device,
-                     q_lens=[300, 64, 1000])
+                     q_lens=[300, 64, 1000], prefix=64)
     write(c)
     ref, rows = oracle_prefill(c)
-    _lib.lib().flour_hip_set_prefill_precise_p(0)
+    _lib.lib().flour_hip_set_prefill_precise_p(1)
     try:
         got = to_np(run(c, torch.float32))[rows]
     finally:
-        _lib.lib().flour_hip_set_prefill_precise_p(1)
+        _lib.lib().flour_hip_set_prefill_precise_p(0)
     max_abs, rel = errors(got, ref)
-    print(f"single-rounding P: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
-    assert max_abs <= 2e-2
+    print(f"hi+lo P: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
