@@ -9,25 +9,28 @@
 // head h / n_rep (repeat_kv, cpu.rs:5-13).
 //
 // Design (head_dim 128, block_size a multiple of 16):
-//  * One workgroup (4 waves) per (128-row query tile, query head, sequence); wave w owns 32
-//    query rows. Tiles are issued heaviest first (last query tile of every sequence first),
-//    and the (sequence, head) order inside one tile rank is permuted so that the heads that
-//    share a kv head land on the same XCD (same L2) — the hardware deals workgroups to the 8
-//    XCDs round-robin.
-//  * 64-token K/V tiles are gathered page by page through the block table into LDS; the
-//    global loads of tile t+1 are in flight while tile t is computed. K is stored row-major
+//  * One workgroup (8 waves) per (128-row query tile, pair of query heads that share a kv
+//    head, sequence); wave w owns 32 query rows of head w / 4, and every K/V tile staged in
+//    LDS serves both heads. Workgroups are issued in decreasing query-tile index (close to
+//    longest-first, spread over all XCDs).
+//  * 64-token K/V tiles are gathered page by page through the block table into LDS with
+//    buffer loads (tokens past kv_len read zeros); the loads of tile t+2 are in flight while
+//    tile t is computed and tile t+1 is written to the other LDS buffer. K is stored row-major
 //    (pitch 272 B, conflict-free 16 B reads); V is stored transposed (V^T, pitch 144 B) with the
 //    tokens of each 16-token group permuted (bits 2 and 3 swapped), which is the order in which
 //    the score registers feed the P.V product.
 //  * S^T = K Q^T on v_mfma_f32_32x32x16 (M = 32 tokens, N = 32 queries, K = 16 dims): lane
 //    (h, q) = (lane/32, lane%32) holds query q's scores for tokens 8i + 4h + j. Those registers
-//    are, after bf16 packing, the B operand of O^T = V^T P^T (K = 16 tokens), so P never moves
-//    between lanes; V^T rows come straight from LDS as 16 B reads.
-//  * Online softmax in the exp2 domain, one max exchange between the two lane halves per tile;
-//    the output accumulator is rescaled only when some lane's max moved. Fully masked tiles
-//    are skipped per wave, masks are evaluated only on tiles that cross the diagonal.
-//  * PRECISE_P: P is split into hi + lo 16-bit parts (two MFMAs per product), keeping ~16
-//    mantissa bits of the softmax weights; otherwise P is rounded once to 16 bits.
+//    are, after 16-bit packing, the B operand of O^T = V^T P^T (K = 16 tokens), so P never
+//    moves between lanes; V^T rows come straight from LDS as 16 B reads.
+//  * Online softmax in the exp2 domain with the scale folded into the exponent's FMA (the
+//    MFMA path requires scale > 0), one max exchange between the two lane halves per tile.
+//    The reference max may lag the running max by up to 8 (weights up to 2^8), so the output
+//    accumulator is rescaled only when some row's max grows past that. Fully masked tiles are
+//    skipped per wave; masks are evaluated only on tiles that cross the diagonal.
+//  * P.V precision: PV_F16 rounds P once to fp16 and widens bf16 V to fp16 (exact in range);
+//    PV_HILO splits P into hi + lo parts of the storage type (two MFMAs per product, ~16
+//    significant bits).
 #include <math.h>
 
 #include <type_traits>
@@ -77,23 +80,25 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int64_t q_sh, const T* __restrict__ k_pool, const T* __restrict__ v_pool,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ block_tables, int max_blocks, int num_seqs, int num_heads,
-    int n_rep, int block_size, int64_t num_slots, float scale_log2) {
+    int n_rep, int block_size, int64_t num_slots, int n_qt_max, float scale_log2) {
     constexpr int D = PF_D;
     // V^T is staged as fp16 for PV_F16, as the storage type otherwise; K keeps the storage type.
     typedef typename std::conditional<PV == PV_F16, f16_t, T>::type TV;
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][PF_KT * PF_KPITCH];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][PF_D * PF_VPITCH];
 
-    // ---- work item: (query tile from the end, sequence, pair of query heads)
+    // ---- work item: (query tile, sequence, pair of query heads). Workgroups are issued in
+    // decreasing query-tile index: the cost of a tile grows with its index (its causal kv range
+    // is kv_len - q_len + 128 (qt + 1)), so this is close to longest-first order, and every
+    // tile level is spread over all XCDs (the dispatcher deals workgroups to the 8 XCDs
+    // round-robin). Items past a sequence's last tile exit at once.
     const int pairs_per_kv = (n_rep + 1) >> 1;
     const int kv_heads = num_heads / n_rep;
-    const int per_rank = num_seqs * kv_heads * pairs_per_kv;
-    const int bid = blockIdx.x;
-    const int tile_rev = bid / per_rank;
-    int r = bid - tile_rev * per_rank;
-    const int full8 = per_rank & ~7;
-    if (r < full8) r = (r & 7) * (full8 >> 3) + (r >> 3);
     const int npairs = kv_heads * pairs_per_kv;
+    const int per_rank = num_seqs * npairs;
+    const int bid = blockIdx.x;
+    const int level = bid / per_rank;
+    const int r = bid - level * per_rank;
     const int seq = r / npairs;
     const int hp = r - seq * npairs;
     const int kvh = hp / pairs_per_kv;
@@ -104,9 +109,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // kv lengths are clamped to what the block table can address (a bad length never reads
     // past the table).
     const int kv_len = min(kv_lens[seq], max_blocks * block_size);
-    const int n_qt = (ql + PF_QT - 1) / PF_QT;
-    const int qt = n_qt - 1 - tile_rev;
-    if (qt < 0 || kv_len < ql) return;
+    const int qt = n_qt_max - 1 - level;
+    if (qt * PF_QT >= ql || kv_len < ql) return;
     const int off = kv_len - ql;
     const int row_begin = qt * PF_QT;
     const int row_last = min(row_begin + PF_QT, ql) - 1;
@@ -121,7 +125,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     const int head = kvh * n_rep + 2 * hj + hsel;
     const bool head_ok = 2 * hj + hsel < n_rep;
     const int32_t* bt = block_tables + (int64_t)seq * max_blocks;
-    const int64_t max_phys = num_slots / block_size - 1;
+    const int max_phys = (int)(num_slots / block_size - 1);
     const int last_page = (kv_len - 1) / block_size;
     const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
     const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -147,47 +151,45 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     }
 
     // ---- staging assignment (a 64-token tile is four 16-token groups, each inside one page)
-    // K: two 16 B chunks per thread: token (tid / 16) + 32i of the tile, dims (tid % 16) * 8.
+    // K: two 16 B chunks per thread: token (tid / 16) + 32i of the tile, dims (tid % 16) * 8;
+    //    the group of each chunk, (tid / 256) + 2i, is the same for the whole wave.
     // V: token pair tp = tid % 32 (tokens 2tp, 2tp+1), dims 8dg..8dg+7 with dg = tid / 32;
-    //    stored transposed, token t at column sigma16(t).
+    //    stored transposed, token t at column sigma16(t). Its group tp / 8 varies per lane.
     const int k_row = tid >> 4, k_col = (tid & 15) * 8;
     const int v_tp = tid & 31, v_dg = tid >> 5;
-    // Pool slot of the first token of each group of a tile: workgroup-uniform, read through
-    // the scalar cache.
+    const int k_grp = w >> 2;
+    constexpr uint32_t ROW_BYTES = D * sizeof(T);
+    const uint32_t k_lane = (uint32_t)((k_row & 15) * D + k_col) * (uint32_t)sizeof(T);
+    const uint32_t v_lane = (uint32_t)((2 * v_tp & 15) * D + 8 * v_dg) * (uint32_t)sizeof(T);
+    const bool v_g1 = (v_tp >> 3) & 1, v_g2 = (v_tp >> 4) & 1;
+    // Byte offset (in the kv head's pool) of the first token of each group of a tile:
+    // workgroup-uniform, read through the scalar cache. A bad block id is clamped into the
+    // pool; groups past kv_len reuse the last page (their loads are masked off).
     auto page_bases = [&](int kt, int* pb) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int tok0 = kt * PF_KT + 16 * i;
             const int lb = min(BS16 ? (tok0 >> 4) : tok0 / block_size, last_page);
-            int64_t phys = bt[lb];  // clamped: a bad block id never leaves the pool
-            phys = phys < 0 ? 0 : (phys > max_phys ? max_phys : phys);
-            pb[i] = (int)(phys * block_size + (tok0 - lb * block_size));
+            const int phys = min(max(bt[lb], 0), max_phys);
+            pb[i] = (int)((uint32_t)(phys * block_size + (tok0 - lb * block_size)) * ROW_BYTES);
         }
     };
     // Branch-free tile loads into (kd, vd): tokens past kv_len (or a tile past the last) get an
     // out-of-range offset and read zeros.
     auto gload = [&](int kt, const int* pb, bool valid, u32x4* kd, u32x4* vd) {
-        const int kv0 = kt * PF_KT;
-        const int lim_tok = valid ? kv_len : 0;
+        const int lim_rel = (valid ? kv_len : 0) - kt * PF_KT;  // tile tokens t < lim_rel exist
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int t = k_row + 32 * i;
-            const int g = t >> 4;
-            const int base = g == 0 ? pb[0] : g == 1 ? pb[1] : g == 2 ? pb[2] : pb[3];
-            const uint32_t o = (uint32_t)((base + (t & 15)) * D + k_col) * (uint32_t)sizeof(T);
-            kd[i] = __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, kv0 + t < lim_tok ? o : PF_OOR,
-                                                          0, 0);
+            const uint32_t o = (uint32_t)(k_grp ? pb[2 * i + 1] : pb[2 * i]) + k_lane;
+            kd[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                k_rsrc, k_row + 32 * i < lim_rel ? o : PF_OOR, 0, 0);
         }
-        const int g = v_tp >> 3;
-        const int base = g == 0 ? pb[0] : g == 1 ? pb[1] : g == 2 ? pb[2] : pb[3];
+        const int b01 = v_g1 ? pb[1] : pb[0], b23 = v_g1 ? pb[3] : pb[2];
+        const uint32_t vb = (uint32_t)(v_g2 ? b23 : b01) + v_lane;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int t = 2 * v_tp + j;
-            const uint32_t o =
-                (uint32_t)((base + (t & 15)) * D + 8 * v_dg) * (uint32_t)sizeof(T);
-            vd[j] = __builtin_amdgcn_raw_buffer_load_b128(v_rsrc, kv0 + t < lim_tok ? o : PF_OOR,
-                                                          0, BUF_NT);
-        }
+        for (int j = 0; j < 2; j++)
+            vd[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                v_rsrc, 2 * v_tp + j < lim_rel ? vb + j * ROW_BYTES : PF_OOR, 0, BUF_NT);
     };
     auto lds_store = [&](int buf, u32x4* kd, u32x4* vd) {
 #pragma unroll
@@ -219,22 +221,25 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 #pragma unroll
         for (int y = 0; y < 16; y++) o[x][y] = 0.0f;
 
-    auto compute = [&](int kt, int buf) {
-        const int kv0 = kt * PF_KT;
-        if (!(wave_active && kv0 <= wave_lim)) return;  // uniform per wave
+    // S^T of the tile in flight (64 tokens x 32 queries, two 32-token halves, raw q.k).
+    f32x16 st[2];
+    auto visible = [&](int kt) { return wave_active && kt * PF_KT <= wave_lim; };  // per wave
+    auto qk = [&](int kbuf) __attribute__((always_inline)) {
         // ---- S^T tile (64 tokens x 32 queries) in two 32-token halves, raw q.k
-        f32x16 st[2];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
 #pragma unroll
             for (int y = 0; y < 16; y++) st[mt][y] = 0.0f;
-            const uint16_t* kr = &Ks[buf][(32 * mt + ql32) * PF_KPITCH + 8 * h2];
+            const uint16_t* kr = &Ks[kbuf][(32 * mt + ql32) * PF_KPITCH + 8 * h2];
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) {
                 const u32x4 a = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
                 st[mt] = mfma32x32x16<T>(a, qb[kk], st[mt]);
             }
         }
+    };
+    auto sm_pv = [&](int kt, int vbuf) __attribute__((always_inline)) {
+        const int kv0 = kt * PF_KT;
         // ---- mask, on tiles that cross the diagonal of some row of this wave only. The empty
         // asm statements keep the compiler from if-converting these uniform branches into
         // per-element selects on every tile.
@@ -293,7 +298,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         // ---- O^T += V^T P^T
 #pragma unroll
         for (int mt2 = 0; mt2 < 4; mt2++) {
-            const uint16_t* vr = &Vt[buf][(32 * mt2 + ql32) * PF_VPITCH + 8 * h2];
+            const uint16_t* vr = &Vt[vbuf][(32 * mt2 + ql32) * PF_VPITCH + 8 * h2];
 #pragma unroll
             for (int kk2 = 0; kk2 < 4; kk2++) {
                 const u32x4 a = *reinterpret_cast<const u32x4*>(vr + 16 * kk2);
@@ -318,13 +323,16 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     auto step = [&](int kt, u32x4* knx, u32x4* vnx, u32x4* kst1, u32x4* vst1) {
         gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
         page_bases(min(kt + 3, n_kt - 1), pb0);
-        compute(kt, kt & 1);
+        if (visible(kt)) {
+            qk(kt & 1);
+            sm_pv(kt, kt & 1);
+        }
         lds_store((kt + 1) & 1, kst1, vst1);
 #pragma unroll
         for (int i = 0; i < 4; i++) {  // pb2 <- tile kt + 3
-            const int t = pb2[i];
+            const int x = pb2[i];
             pb2[i] = pb0[i];
-            pb0[i] = t;
+            pb0[i] = x;
         }
         __syncthreads();
     };
@@ -373,7 +381,7 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
     kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
         static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
         static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt, max_blocks,
-        num_seqs, num_heads, n_rep, block_size, num_slots, scale * PF_LOG2E);
+        num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt, scale * PF_LOG2E);
     return check_hip(hipGetLastError(), "varlen_prefill launch");
 }
 
