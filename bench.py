@@ -45,7 +45,28 @@ def parse_args():
     ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run plain 1 GiB device copies (a known-size reference for the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
+
+
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """Three device-to-device copies of COPY_BYTES each: every launch reads and writes exactly
+    COPY_BYTES, which scales the HBM byte counters of the profiler."""
+    import torch
+
+    a = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda:0")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "launches": 3}), flush=True)
 
 
 def event_timed(torch, fn, steps: int, warmup: int):
@@ -193,8 +214,43 @@ def bench_prefill(torch, ops, case, steps, warmup):
                 causal_pairs=case.causal_pairs())
 
 
+def prefill_line(torch, ops, case, name, cfg, args):
+    """One JSON line for a prefill workload (KV write + causal varlen prefill per step)."""
+    r = bench_prefill(torch, ops, case, args.steps, args.warmup)
+    line = {
+        "metric": "causal varlen prefill attention throughput (useful causal FLOPs)",
+        "value": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1); random slot mapping into a 1.25x pool)",
+        "config": {"workload": name, "num_seqs": cfg["num_seqs"], "num_heads": cfg["num_heads"],
+                   "kv_heads": cfg["kv_heads"], "head_dim": cfg["head_dim"],
+                   "block_size": cfg["block_size"], "q_len": f"U[{cfg['q_len'][0]},{cfg['q_len'][1]}]",
+                   "prefix": cfg["prefix"], "flops_per_step": r["flops"]},
+        "roofline": {"bound": "mfma", "kernel": "varlen_prefill_mfma_kernel",
+                     "achieved": round(r["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
+                     "avg_launch_us": round(r["attn_ms"] * 1e3, 3), "traffic": read_traffic(name)},
+        "kv_write": {"GB/s": round(r["write_gbs"], 1), "avg_launch_us": round(r["write_ms"] * 1e3, 3),
+                     "bytes": r["write_bytes"]},
+    }
+    if not args.no_cpu:
+        tf, th, reps, S, P = cpu_prefill_baseline(case, args.cpu_seconds)
+        line["cpu_baseline"] = {"value": round(tf, 5), "unit": "TFLOP/s", "cores": th, "kind": "port",
+                                "sample": f"shortest sequence of the batch (q_len {S}, prefix {P}), "
+                                          f"median of {reps} runs of the C restatement of "
+                                          "cpu.rs:57-112"}
+    else:
+        line["cpu_baseline"] = None
+    return line
+
+
 def main():
     args = parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every kernel of "
               "this path runs on a single MI355X; the multi-GPU sharding is a design note only).",
@@ -211,7 +267,8 @@ def main():
     case = make_workload(name, device=dev)
     torch.cuda.synchronize()
     if cfg["kind"] != "decode":
-        raise SystemExit("the headline workload must be a decode workload")
+        print(json.dumps(prefill_line(torch, ops, case, name, cfg, args)), flush=True)
+        return
     r = bench_decode(torch, ops, case, args.steps, args.warmup)
     value = r["gbs_step"]
 
@@ -236,7 +293,7 @@ def main():
             "algorithmic_bytes_per_step": r["bytes"], "out_dtype": "bf16",
         },
         "roofline": {
-            "bound": "hbm", "kernel": "paged_decode_mfma_kernel",
+            "bound": "hbm", "kernel": "paged_decode_mfma_kernel + paged_decode_merge_kernel",
             "achieved": round(r["gbs_kernel"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
             "avg_launch_us": round(r["kernel_ms"] * 1e3, 3),
