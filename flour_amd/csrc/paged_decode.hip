@@ -7,23 +7,24 @@
 // the causal mask of cpu.rs:88-95 admits every cached position, so only positions past the
 // context length are masked.
 //
-// Work decomposition (stream-K): the K/V to read is the list of 32-token chunks of every
-// (sequence, kv head) pair, laid end to end. One resident round of workgroups (2 per CU) each
-// takes an equal contiguous range of that list, so every CU streams the same number of bytes
-// whatever the spread of context lengths, and no workgroup pays a launch or a ramp-up twice.
-// A pair wholly inside one range is finished by its workgroup; a pair cut by range ends leaves
-// one partial (max, sum, acc) row per piece, and a small second kernel on the same stream
-// merges those (log-sum-exp merge, as in the running update of cpu.rs:96-105). The kernel
-// boundary orders partial writes before merge reads; an in-kernel "last workgroup merges"
-// scheme would need an agent-scope release/acquire per workgroup, which on this multi-XCD part
-// writes back and invalidates the XCD's L2 each time.
+// Work decomposition (stream-K at wave granularity): the K/V to read is the list of 32-token
+// chunks of every (sequence, kv head) pair, laid end to end. One resident round of one-wave
+// workgroups (8 per CU, 2 per SIMD) each takes an equal contiguous range of that list, so every
+// wave streams the same number of bytes whatever the spread of context lengths, and no wave
+// pays a launch or a ramp-up twice. A pair wholly inside one range is finished by its wave; a
+// pair cut by range ends leaves one partial (max, sum, acc) row per piece, and a small second
+// kernel on the same stream merges those (log-sum-exp merge, as in the running update of
+// cpu.rs:96-105). The kernel boundary orders partial writes before merge reads; an in-kernel
+// "last workgroup merges" scheme would need an agent-scope release/acquire per workgroup,
+// which on this multi-XCD part writes back and invalidates the XCD's L2 each time.
 //
 // Inside a piece (bf16/f16 pools, head_dim 128, block_size a multiple of 16):
-//  * The 4 waves take the piece's chunks round robin. A chunk is two 16-token MFMA tiles, each
-//    one 4 KB (head, 16 slots) pool run of K and of V, read with non-temporal buffer loads
-//    (per-pool resource, loop-invariant lane offset, per-tile SGPR offset); two register
-//    buffers ping-pong so the next chunk's loads are in flight while one is computed. Every
-//    query head of the kv head shares each K/V load (GQA reuse: K/V leave HBM once).
+//  * The wave walks its piece chunk by chunk. A chunk is two 16-token MFMA tiles, each one
+//    4 KB (head, 16 slots) pool run of K and of V, read with buffer loads (per-pool resource,
+//    loop-invariant lane offset, per-tile SGPR offset; V non-temporal); two register buffers
+//    ping-pong so the next chunk's loads are in flight while one is computed, with the loop
+//    peeled so that no load is conditional. Every query head of the kv head shares each K/V
+//    load (GQA reuse: K/V leave HBM once).
 //  * Scores S = K Q^T on v_mfma_f32_16x16x32 (M = 16 tokens, N = 16 query-head columns, the
 //    n_rep real heads padded with zero rows): lane (g, c) = (lane/16, lane%16) holds head c's
 //    scores for tokens 4g..4g+3 of each tile.
@@ -58,14 +59,14 @@ static constexpr float LOG2E = 1.4426950408889634f;
 static constexpr int DEC_CHUNK = 32;         // tokens per step (two 16-token MFMA tiles)
 static constexpr int DEC_SEG = 32;           // chunks per tile-slot refill (64 tiles, one per lane)
 static constexpr int DEC_MAX_BATCH = 4096;   // per-sequence chunk prefix sums live in LDS
-static constexpr int DEC_WAVES_PER_CU = 8;
+static constexpr int DEC_WAVES_PER_CU = 8;  // 2 per SIMD: the register budget of the kernel
 // K rows are read as two 64 B halves of each 128 B line by back-to-back instructions; a
 // cached load lets the second half hit the line the first brought in, which measures faster
 // than the non-temporal hint that suits the fully coalesced V rows.
 #ifndef FLOUR_DEC_K_POLICY
 #define FLOUR_DEC_K_POLICY 0
 #endif
-static constexpr int K_POLICY = FLOUR_DEC_K_POLICY;   // 2 per SIMD: the register budget of the kernel
+static constexpr int K_POLICY = FLOUR_DEC_K_POLICY;
 
 struct DecodeWs {
     float* ml;  // [2 * num_waves][n_rep][2] (max, sum) in the exp2 domain
