@@ -237,6 +237,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 st[mt] = mfma32x32x16<T>(a, qb[kk], st[mt]);
             }
         }
+        // issue order: the first half's K reads, then each product followed by one read of
+        // the second half's K
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
     };
     auto sm_pv = [&](int kt, int vbuf) __attribute__((always_inline)) {
         const int kv0 = kt * PF_KT;
@@ -270,14 +278,15 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             for (int x = 0; x < 4; x++) o[x] *= alpha;
             m = m_new;
         }
-        // ---- p = 2^(s * scale_log2 - m), one FMA + exp per score, then the P^T B operands:
-        // kk2 covers tokens of half kk2/2, rows i = 2(kk2&1), +1. The row sum is taken over the
-        // rounded weights that enter the product (v_dot2 over fp16 pairs) in PV_F16 mode.
+        // ---- p = 2^(s * scale_log2 - m), one FMA + exp per score, packed as the P^T B operand
+        // of step kk2 (tokens of half kk2/2, rows i = 2(kk2&1), +1); then O^T += V^T P^T in
+        // kk2-major order, so that the exps of step kk2+1 and the V reads of step kk2+1 can run
+        // under the matrix products of step kk2. The row sum is taken over the rounded weights
+        // that enter the product (v_dot2 over fp16 pairs) in PV_F16 mode.
         const float nm = -m;
         u32x4 pb_hi[4], pb_lo[4];
         float psum = 0.0f;
-#pragma unroll
-        for (int kk2 = 0; kk2 < 4; kk2++) {
+        auto weights = [&](int kk2) __attribute__((always_inline)) {
             const int mt = kk2 >> 1, y0 = 8 * (kk2 & 1);
 #pragma unroll
             for (int x = 0; x < 4; x++) {
@@ -293,17 +302,40 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                                                   false);
                 }
             }
+        };
+        const uint16_t* vr = &Vt[vbuf][ql32 * PF_VPITCH + 8 * h2];
+        u32x4 vf[2][4];
+#pragma unroll
+        for (int mt2 = 0; mt2 < 4; mt2++)
+            vf[0][mt2] = *reinterpret_cast<const u32x4*>(vr + 32 * mt2 * PF_VPITCH);
+        weights(0);
+#pragma unroll
+        for (int kk2 = 0; kk2 < 4; kk2++) {
+            if (kk2 < 3) {
+#pragma unroll
+                for (int mt2 = 0; mt2 < 4; mt2++)
+                    vf[(kk2 + 1) & 1][mt2] = *reinterpret_cast<const u32x4*>(
+                        vr + 32 * mt2 * PF_VPITCH + 16 * (kk2 + 1));
+                weights(kk2 + 1);
+            }
+#pragma unroll
+            for (int mt2 = 0; mt2 < 4; mt2++) {
+                o[mt2] = mfma32x32x16<TV>(vf[kk2 & 1][mt2], pb_hi[kk2], o[mt2]);
+                if constexpr (PV == PV_HILO)
+                    o[mt2] = mfma32x32x16<TV>(vf[kk2 & 1][mt2], pb_lo[kk2], o[mt2]);
+            }
         }
         lsum += psum;
-        // ---- O^T += V^T P^T
+        if constexpr (PV == PV_F16) {
+            // issue order: V reads and weights of step 0, then each product followed by a
+            // share of the next step's VALU work and one V read
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x402, 24, 0);
 #pragma unroll
-        for (int mt2 = 0; mt2 < 4; mt2++) {
-            const uint16_t* vr = &Vt[vbuf][(32 * mt2 + ql32) * PF_VPITCH + 8 * h2];
-#pragma unroll
-            for (int kk2 = 0; kk2 < 4; kk2++) {
-                const u32x4 a = *reinterpret_cast<const u32x4*>(vr + 16 * kk2);
-                o[mt2] = mfma32x32x16<TV>(a, pb_hi[kk2], o[mt2]);
-                if constexpr (PV == PV_HILO) o[mt2] = mfma32x32x16<TV>(a, pb_lo[kk2], o[mt2]);
+            for (int i = 0; i < 16; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if (i < 12) __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
             }
         }
     };
