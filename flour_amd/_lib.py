@@ -39,6 +39,43 @@ SIGNATURES: dict[str, tuple] = {
                                           _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                           _c_int, _c_int, _c_int, _c_int, _c_i64, _c_f, _c_int,
                                           _vp]),
+    # include/flour_cache.h
+    "flour_block_allocator_create": (_c_int, [_c_int, _vp]),
+    "flour_block_allocator_destroy": (None, [_vp]),
+    "flour_block_allocator_allocate": (_c_int, [_vp]),
+    "flour_block_allocator_incref": (_c_int, [_vp, _c_int]),
+    "flour_block_allocator_decref": (_c_int, [_vp, _c_int]),
+    "flour_block_allocator_ref_count": (_c_int, [_vp, _c_int]),
+    "flour_block_allocator_num_free": (_c_int, [_vp]),
+    "flour_block_table_create": (_c_int, [_c_int, _vp]),
+    "flour_block_table_destroy": (None, [_vp]),
+    "flour_block_table_push_block": (_c_int, [_vp, _c_int]),
+    "flour_block_table_advance": (_c_int, [_vp, _c_int]),
+    "flour_block_table_clear": (_c_int, [_vp]),
+    "flour_block_table_len": (_c_int, [_vp]),
+    "flour_block_table_capacity": (_c_int, [_vp]),
+    "flour_block_table_block_size": (_c_int, [_vp]),
+    "flour_block_table_blocks": (_c_int, [_vp, _vp, _c_int, _vp]),
+    "flour_block_table_slot": (_c_i64, [_vp, _c_int]),
+    "flour_block_table_slots": (_c_int, [_vp, _c_int, _c_int, _vp]),
+    "flour_kv_cache_create": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                       _c_int, _vp]),
+    "flour_kv_cache_destroy": (None, [_vp]),
+    "flour_kv_cache_allocate_kv": (_c_int, [_vp, _c_int]),
+    "flour_kv_cache_len": (_c_int, [_vp]),
+    "flour_kv_cache_capacity": (_c_int, [_vp]),
+    "flour_kv_cache_free_blocks": (_c_int, [_vp]),
+    "flour_kv_cache_ref_count": (_c_int, [_vp, _c_int]),
+    "flour_kv_cache_blocks": (_c_int, [_vp, _vp, _c_int, _vp]),
+    "flour_kv_cache_slots": (_c_int, [_vp, _c_int, _c_int, _vp]),
+    "flour_kv_cache_write_kv": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_i64, _c_i64, _vp]),
+    "flour_kv_cache_attention": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_i64, _c_i64, _vp,
+                                          _c_int, _c_i64, _c_i64, _c_f, _vp]),
+    "flour_kv_cache_reset_sequence": (_c_int, [_vp]),
+    "flour_kv_cache_match_prefix": (_c_int, [_vp, _vp, _c_int]),
+    "flour_kv_cache_register_prefix": (_c_int, [_vp, _vp, _c_int]),
+    "flour_kv_cache_clear_prefix_cache": (_c_int, [_vp]),
+    "flour_kv_cache_pool": (_c_int, [_vp, _c_int, _vp, _vp, _vp]),
 }
 
 

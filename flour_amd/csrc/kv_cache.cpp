@@ -1,0 +1,617 @@
+// kv_cache.cpp — host-side KV-cache bookkeeping over a device pool (include/flour_cache.h).
+//
+// Restates the reference's per-sequence cache: BlockAllocator and BlockTable
+// (src/models/common/paged.rs:7-121), the prefix registry (src/models/common/prefix.rs:1-60)
+// and KvCache / Cache (src/models/common/cache.rs:13-165, :429-505), with the pool of
+// PagedKvPool::new (paged.rs:138-167) in device memory. The attention call marshals the live
+// block table to the device and launches the kernels of flour_hip.h, which replaces
+// Cache::kv_blocks + paged_attention (attention.rs:104-109).
+//
+// Block hashes: a chained 64-bit hash of (parent hash, the block's token ids), so equal
+// hashes identify equal full-prefix paths; as in prefix.rs the registry keeps each block's
+// tokens and rejects a lookup whose tokens differ (hash collisions never return wrong KV).
+// The hash function is this file's own (the reference uses Rust's DefaultHasher); only the
+// identity of prefix paths matters, the values are never stored outside the process.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <unordered_map>
+#include <vector>
+
+#include "flour_cache.h"
+#include "flour_common.h"
+#include "flour_hip.h"
+
+namespace flour {
+namespace host {
+
+// ---------------------------------------------------------------- BlockAllocator
+class BlockAllocator {
+  public:
+    explicit BlockAllocator(int n) : refs_(n, 0) {
+        free_.reserve(n);
+        for (int i = n - 1; i >= 0; i--) free_.push_back(i);  // first allocate returns 0
+    }
+    int allocate() {
+        if (free_.empty()) return -1;
+        const int id = free_.back();
+        free_.pop_back();
+        refs_[id] = 1;
+        return id;
+    }
+    bool valid(int id) const { return id >= 0 && id < (int)refs_.size(); }
+    void incref(int id) { refs_[id]++; }
+    // true when the block reached zero references and returned to the free list
+    bool decref(int id) {
+        if (--refs_[id] == 0) {
+            free_.push_back(id);
+            return true;
+        }
+        return false;
+    }
+    int ref_count(int id) const { return refs_[id]; }
+    int num_free() const { return (int)free_.size(); }
+    int num_blocks() const { return (int)refs_.size(); }
+
+  private:
+    std::vector<int> free_;
+    std::vector<int> refs_;
+};
+
+// ---------------------------------------------------------------- BlockTable
+class BlockTable {
+  public:
+    explicit BlockTable(int bs) : bs_(bs) {}
+    int len() const { return len_; }
+    int block_size() const { return bs_; }
+    int capacity() const { return (int)blocks_.size() * bs_; }
+    void push_block(int id) { blocks_.push_back(id); }
+    const std::vector<int>& blocks() const { return blocks_; }
+    int block_at(int i) const { return blocks_[i]; }
+    void clear() {
+        blocks_.clear();
+        len_ = 0;
+    }
+    void advance(int n) { len_ += n; }
+    int64_t slot(int pos) const { return (int64_t)blocks_[pos / bs_] * bs_ + pos % bs_; }
+    bool backed(int pos) const { return pos >= 0 && pos / bs_ < (int)blocks_.size(); }
+
+  private:
+    std::vector<int> blocks_;
+    int bs_;
+    int len_ = 0;
+};
+
+// ---------------------------------------------------------------- prefix registry
+static constexpr uint64_t PREFIX_SEED = 0;
+
+static inline uint64_t mix64(uint64_t z) {  // splitmix64 finaliser
+    z ^= z >> 30;
+    z *= 0xbf58476d1ce4e5b9ull;
+    z ^= z >> 27;
+    z *= 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// Chained block hash: identifies the full prefix path ending with this block.
+static uint64_t block_hash(uint64_t parent, const uint32_t* tok, int n) {
+    uint64_t h = mix64(parent ^ 0x9e3779b97f4a7c15ull) ^ (uint64_t)n;
+    for (int i = 0; i < n; i++) h = mix64(h ^ ((uint64_t)tok[i] + 0x632be59bd9b4e019ull));
+    return h;
+}
+
+struct RegistryEntry {
+    std::vector<uint32_t> tokens;
+    int block_id;
+};
+
+class PrefixRegistry {
+  public:
+    // block id stored under `h`, only when its tokens equal `tok` (collisions are misses)
+    int get(uint64_t h, const uint32_t* tok, int n) const {
+        auto it = map_.find(h);
+        if (it == map_.end() || (int)it->second.tokens.size() != n ||
+            memcmp(it->second.tokens.data(), tok, n * sizeof(uint32_t)) != 0)
+            return -1;
+        return it->second.block_id;
+    }
+    bool contains(uint64_t h) const { return map_.count(h) != 0; }
+    void insert(uint64_t h, const uint32_t* tok, int n, int id) {
+        map_[h] = RegistryEntry{std::vector<uint32_t>(tok, tok + n), id};
+    }
+    std::vector<int> drain_block_ids() {
+        std::vector<int> ids;
+        ids.reserve(map_.size());
+        for (auto& kv : map_) ids.push_back(kv.second.block_id);
+        map_.clear();
+        return ids;
+    }
+
+  private:
+    std::unordered_map<uint64_t, RegistryEntry> map_;
+};
+
+// ---------------------------------------------------------------- KvCache + device pool
+struct KvCacheImpl {
+    int num_layers, max_seq_len, num_heads, kv_heads, head_dim, block_size, dtype;
+    int num_blocks;
+    int64_t num_slots;
+    BlockAllocator allocator;
+    BlockTable table;
+    PrefixRegistry registry;
+
+    bool device = false;
+    std::vector<void*> k_pools, v_pools;  // per layer, (kv_heads, num_slots, head_dim)
+    // device inputs of the kernels: [0, num_blocks) block table, then kv_len, cu_seqlens (2),
+    // then the slot mapping of the current batch (max_seq_len entries)
+    int32_t* d_meta = nullptr;
+    int32_t* h_meta = nullptr;  // pinned staging of the same layout
+    hipEvent_t meta_done = nullptr;
+    bool meta_pending = false;
+    void* d_ws = nullptr;
+    size_t ws_bytes = 0;
+    uint64_t table_version = 1, uploaded_version = 0;
+    int uploaded_len = -1;
+
+    KvCacheImpl(int L, int max_len, int H, int G, int D, int bs, int dt)
+        : num_layers(L),
+          max_seq_len(max_len),
+          num_heads(H),
+          kv_heads(G),
+          head_dim(D),
+          block_size(bs),
+          dtype(dt),
+          num_blocks((max_len + bs - 1) / bs),
+          num_slots((int64_t)((max_len + bs - 1) / bs) * bs),
+          allocator((max_len + bs - 1) / bs),
+          table(bs) {}
+
+    int meta_ints() const { return num_blocks + 3 + max_seq_len; }
+    int32_t* d_table() const { return d_meta; }
+    int32_t* d_kv_len() const { return d_meta + num_blocks; }
+    int32_t* d_cu() const { return d_meta + num_blocks + 1; }
+    int32_t* d_slots() const { return d_meta + num_blocks + 3; }
+
+    ~KvCacheImpl() {
+        if (meta_done) {
+            if (meta_pending) (void)hipEventSynchronize(meta_done);
+            (void)hipEventDestroy(meta_done);
+        }
+        for (void* p : k_pools)
+            if (p) (void)hipFree(p);
+        for (void* p : v_pools)
+            if (p) (void)hipFree(p);
+        if (d_meta) (void)hipFree(d_meta);
+        if (h_meta) (void)hipHostFree(h_meta);
+        if (d_ws) (void)hipFree(d_ws);
+    }
+
+    int alloc_device() {
+        const size_t pool_bytes = (size_t)kv_heads * num_slots * head_dim * elem_bytes(dtype);
+        k_pools.assign(num_layers, nullptr);
+        v_pools.assign(num_layers, nullptr);
+        for (int l = 0; l < num_layers; l++) {
+            if (check_hip(hipMalloc(&k_pools[l], pool_bytes), "kv_cache: pool allocation") ||
+                check_hip(hipMalloc(&v_pools[l], pool_bytes), "kv_cache: pool allocation") ||
+                check_hip(hipMemset(k_pools[l], 0, pool_bytes), "kv_cache: pool zero fill") ||
+                check_hip(hipMemset(v_pools[l], 0, pool_bytes), "kv_cache: pool zero fill"))
+                return FLOUR_ERR_HIP;
+        }
+        const size_t meta_bytes = (size_t)meta_ints() * sizeof(int32_t);
+        if (check_hip(hipMalloc(&d_meta, meta_bytes), "kv_cache: table allocation") ||
+            check_hip(hipHostMalloc(&h_meta, meta_bytes, hipHostMallocDefault),
+                      "kv_cache: pinned staging") ||
+            check_hip(hipEventCreateWithFlags(&meta_done, hipEventDisableTiming),
+                      "kv_cache: event"))
+            return FLOUR_ERR_HIP;
+        if (flour_hip_paged_decode_workspace_size(1, num_heads, kv_heads, head_dim, max_seq_len,
+                                                  &ws_bytes) != FLOUR_OK)
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        if (ws_bytes && check_hip(hipMalloc(&d_ws, ws_bytes), "kv_cache: decode workspace"))
+            return FLOUR_ERR_HIP;
+        device = true;
+        return FLOUR_OK;
+    }
+
+    // Wait until the previous upload has read the pinned staging buffer before rewriting it.
+    int staging_ready() {
+        if (!meta_pending) return FLOUR_OK;
+        meta_pending = false;
+        return check_hip(hipEventSynchronize(meta_done), "kv_cache: staging wait");
+    }
+
+    // Copy ints [first, first + count) of the staging layout to the device on `s`.
+    int upload(int first, int count, hipStream_t s) {
+        if (check_hip(hipMemcpyAsync(d_meta + first, h_meta + first, count * sizeof(int32_t),
+                                     hipMemcpyHostToDevice, s),
+                      "kv_cache: table upload") ||
+            check_hip(hipEventRecord(meta_done, s), "kv_cache: event record"))
+            return FLOUR_ERR_HIP;
+        meta_pending = true;
+        return FLOUR_OK;
+    }
+
+    // Block table, live length and cu_seqlens for an attention call over seq_q rows.
+    int upload_table(int seq_q, hipStream_t s) {
+        const int len = table.len();
+        if (uploaded_version == table_version && uploaded_len == len && h_meta[num_blocks + 2] == seq_q)
+            return FLOUR_OK;
+        int rc = staging_ready();
+        if (rc) return rc;
+        const auto& b = table.blocks();
+        for (int i = 0; i < (int)b.size(); i++) h_meta[i] = b[i];
+        for (int i = (int)b.size(); i < num_blocks; i++) h_meta[i] = 0;
+        h_meta[num_blocks] = len;
+        h_meta[num_blocks + 1] = 0;
+        h_meta[num_blocks + 2] = seq_q;
+        rc = upload(0, num_blocks + 3, s);
+        if (rc) return rc;
+        uploaded_version = table_version;
+        uploaded_len = len;
+        return FLOUR_OK;
+    }
+
+    // ---- KvCache operations
+    int allocate_kv(int seq_len) {
+        const int64_t end = (int64_t)table.len() + seq_len;
+        if (seq_len < 0) {
+            set_error("kv_cache: negative seq_len %d", seq_len);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (end > max_seq_len) {
+            set_error("paged kv cache overflow: %lld tokens exceeds max_seq_len %d",
+                      (long long)end, max_seq_len);
+            return FLOUR_ERR_CAPACITY;
+        }
+        while (table.capacity() < end) {
+            const int id = allocator.allocate();
+            if (id < 0) {
+                set_error("out of kv blocks");
+                return FLOUR_ERR_OUT_OF_BLOCKS;
+            }
+            table.push_block(id);
+            table_version++;
+        }
+        table.advance(seq_len);
+        return FLOUR_OK;
+    }
+
+    void reset_sequence() {
+        for (int id : table.blocks()) allocator.decref(id);
+        table.clear();
+        table_version++;
+    }
+
+    int match_prefix(const uint32_t* tok, int n) {
+        const int bs = table.block_size();
+        const int full = n / bs;
+        const int reusable = (n % bs == 0) ? (full > 0 ? full - 1 : 0) : full;
+        uint64_t parent = PREFIX_SEED;
+        int matched = 0;
+        for (int b = 0; b < reusable; b++) {
+            const uint32_t* chunk = tok + (int64_t)b * bs;
+            const uint64_t h = block_hash(parent, chunk, bs);
+            const int id = registry.get(h, chunk, bs);
+            if (id < 0) break;
+            allocator.incref(id);
+            table.push_block(id);
+            table_version++;
+            matched += bs;
+            parent = h;
+        }
+        table.advance(matched);
+        return matched;
+    }
+
+    int register_prefix(const uint32_t* tok, int n) {
+        const int bs = table.block_size();
+        const int full = n / bs;
+        if (full > (int)table.blocks().size()) {
+            set_error("kv_cache: register_prefix over %d full blocks, the sequence holds %d", full,
+                      (int)table.blocks().size());
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        uint64_t parent = PREFIX_SEED;
+        for (int b = 0; b < full; b++) {
+            const uint32_t* chunk = tok + (int64_t)b * bs;
+            const uint64_t h = block_hash(parent, chunk, bs);
+            if (!registry.contains(h)) {
+                const int id = table.block_at(b);
+                allocator.incref(id);  // the registry holds its own reference
+                registry.insert(h, chunk, bs, id);
+            }
+            parent = h;
+        }
+        return FLOUR_OK;
+    }
+
+    void clear_prefix_cache() {
+        for (int id : registry.drain_block_ids()) allocator.decref(id);
+    }
+};
+
+}  // namespace host
+}  // namespace flour
+
+using namespace flour;
+using namespace flour::host;
+
+struct flour_block_allocator {
+    BlockAllocator a;
+};
+struct flour_block_table {
+    BlockTable t;
+};
+struct flour_kv_cache {
+    KvCacheImpl c;
+};
+
+#define FLOUR_NEED(cond, ...)                         \
+    do {                                              \
+        if (!(cond)) {                                \
+            set_error(__VA_ARGS__);                   \
+            return FLOUR_ERR_INVALID_ARGUMENT;        \
+        }                                             \
+    } while (0)
+
+// ---------------------------------------------------------------- allocator C-ABI
+extern "C" int flour_block_allocator_create(int num_blocks, flour_block_allocator** out) {
+    clear_error();
+    FLOUR_NEED(out && num_blocks >= 0, "block_allocator: bad arguments");
+    *out = new flour_block_allocator{BlockAllocator(num_blocks)};
+    return FLOUR_OK;
+}
+extern "C" void flour_block_allocator_destroy(flour_block_allocator* a) { delete a; }
+extern "C" int flour_block_allocator_allocate(flour_block_allocator* a) {
+    clear_error();
+    FLOUR_NEED(a, "block_allocator: null");
+    return a->a.allocate();
+}
+extern "C" int flour_block_allocator_incref(flour_block_allocator* a, int id) {
+    clear_error();
+    FLOUR_NEED(a && a->a.valid(id), "block_allocator: unknown block %d", id);
+    a->a.incref(id);
+    return FLOUR_OK;
+}
+extern "C" int flour_block_allocator_decref(flour_block_allocator* a, int id) {
+    clear_error();
+    FLOUR_NEED(a && a->a.valid(id), "block_allocator: unknown block %d", id);
+    FLOUR_NEED(a->a.ref_count(id) > 0, "decref of unreferenced block %d", id);
+    return a->a.decref(id) ? 1 : 0;
+}
+extern "C" int flour_block_allocator_ref_count(const flour_block_allocator* a, int id) {
+    clear_error();
+    FLOUR_NEED(a && a->a.valid(id), "block_allocator: unknown block %d", id);
+    return a->a.ref_count(id);
+}
+extern "C" int flour_block_allocator_num_free(const flour_block_allocator* a) {
+    clear_error();
+    FLOUR_NEED(a, "block_allocator: null");
+    return a->a.num_free();
+}
+
+// ---------------------------------------------------------------- block table C-ABI
+extern "C" int flour_block_table_create(int block_size, flour_block_table** out) {
+    clear_error();
+    FLOUR_NEED(out && block_size > 0, "block_table: bad arguments");
+    *out = new flour_block_table{BlockTable(block_size)};
+    return FLOUR_OK;
+}
+extern "C" void flour_block_table_destroy(flour_block_table* t) { delete t; }
+extern "C" int flour_block_table_push_block(flour_block_table* t, int id) {
+    clear_error();
+    FLOUR_NEED(t && id >= 0, "block_table: bad block id %d", id);
+    t->t.push_block(id);
+    return FLOUR_OK;
+}
+extern "C" int flour_block_table_advance(flour_block_table* t, int n) {
+    clear_error();
+    FLOUR_NEED(t && n >= 0, "block_table: bad advance %d", n);
+    t->t.advance(n);
+    return FLOUR_OK;
+}
+extern "C" int flour_block_table_clear(flour_block_table* t) {
+    clear_error();
+    FLOUR_NEED(t, "block_table: null");
+    t->t.clear();
+    return FLOUR_OK;
+}
+extern "C" int flour_block_table_len(const flour_block_table* t) { return t ? t->t.len() : -1; }
+extern "C" int flour_block_table_capacity(const flour_block_table* t) {
+    return t ? t->t.capacity() : -1;
+}
+extern "C" int flour_block_table_block_size(const flour_block_table* t) {
+    return t ? t->t.block_size() : -1;
+}
+extern "C" int flour_block_table_blocks(const flour_block_table* t, int32_t* out, int cap,
+                                        int* n) {
+    clear_error();
+    FLOUR_NEED(t && n && (out || cap == 0), "block_table: bad arguments");
+    const auto& b = t->t.blocks();
+    *n = (int)b.size();
+    for (int i = 0; i < (int)b.size() && i < cap; i++) out[i] = b[i];
+    return FLOUR_OK;
+}
+extern "C" int64_t flour_block_table_slot(const flour_block_table* t, int pos) {
+    clear_error();
+    FLOUR_NEED(t && t->t.backed(pos), "block_table: position %d has no block", pos);
+    return t->t.slot(pos);
+}
+extern "C" int flour_block_table_slots(const flour_block_table* t, int start, int end,
+                                       int32_t* out) {
+    clear_error();
+    FLOUR_NEED(t && out && start >= 0 && end >= start && (end == start || t->t.backed(end - 1)),
+               "block_table: slots(%d, %d) outside the mapped blocks", start, end);
+    for (int p = start; p < end; p++) out[p - start] = (int32_t)t->t.slot(p);
+    return FLOUR_OK;
+}
+
+// ---------------------------------------------------------------- kv cache C-ABI
+extern "C" int flour_kv_cache_create(int num_layers, int max_seq_len, int num_heads,
+                                     int kv_heads, int head_dim, int block_size, int dtype,
+                                     int device_pool, flour_kv_cache** out) {
+    clear_error();
+    FLOUR_NEED(out, "kv_cache: null output");
+    *out = nullptr;
+    FLOUR_NEED(num_layers > 0 && max_seq_len > 0 && num_heads > 0 && kv_heads > 0 &&
+                   num_heads % kv_heads == 0 && head_dim > 0 && block_size > 0 &&
+                   valid_dtype(dtype),
+               "kv_cache: bad shape (layers=%d max_seq_len=%d heads=%d kv_heads=%d head_dim=%d "
+               "block_size=%d dtype=%d)",
+               num_layers, max_seq_len, num_heads, kv_heads, head_dim, block_size, dtype);
+    const int64_t slots = (int64_t)((max_seq_len + block_size - 1) / block_size) * block_size;
+    FLOUR_NEED(slots < (1ll << 31), "kv_cache: %lld slots exceed int32 slot ids",
+               (long long)slots);
+    auto* c = new flour_kv_cache{KvCacheImpl(num_layers, max_seq_len, num_heads, kv_heads,
+                                             head_dim, block_size, dtype)};
+    if (device_pool) {
+        const int rc = c->c.alloc_device();
+        if (rc != FLOUR_OK) {
+            delete c;
+            return rc;
+        }
+    }
+    *out = c;
+    return FLOUR_OK;
+}
+extern "C" void flour_kv_cache_destroy(flour_kv_cache* c) { delete c; }
+
+extern "C" int flour_kv_cache_allocate_kv(flour_kv_cache* c, int seq_len) {
+    clear_error();
+    FLOUR_NEED(c, "kv_cache: null");
+    return c->c.allocate_kv(seq_len);
+}
+extern "C" int flour_kv_cache_len(const flour_kv_cache* c) { return c ? c->c.table.len() : -1; }
+extern "C" int flour_kv_cache_capacity(const flour_kv_cache* c) {
+    return c ? c->c.table.capacity() : -1;
+}
+extern "C" int flour_kv_cache_free_blocks(const flour_kv_cache* c) {
+    return c ? c->c.allocator.num_free() : -1;
+}
+extern "C" int flour_kv_cache_ref_count(const flour_kv_cache* c, int id) {
+    clear_error();
+    FLOUR_NEED(c && c->c.allocator.valid(id), "kv_cache: unknown block %d", id);
+    return c->c.allocator.ref_count(id);
+}
+extern "C" int flour_kv_cache_blocks(const flour_kv_cache* c, int32_t* out, int cap, int* n) {
+    clear_error();
+    FLOUR_NEED(c && n && (out || cap == 0), "kv_cache: bad arguments");
+    const auto& b = c->c.table.blocks();
+    *n = (int)b.size();
+    for (int i = 0; i < (int)b.size() && i < cap; i++) out[i] = b[i];
+    return FLOUR_OK;
+}
+extern "C" int flour_kv_cache_slots(const flour_kv_cache* c, int start, int end, int32_t* out) {
+    clear_error();
+    FLOUR_NEED(c && out && start >= 0 && end >= start &&
+                   (end == start || c->c.table.backed(end - 1)),
+               "kv_cache: slots(%d, %d) outside the mapped blocks", start, end);
+    for (int p = start; p < end; p++) out[p - start] = (int32_t)c->c.table.slot(p);
+    return FLOUR_OK;
+}
+
+extern "C" int flour_kv_cache_write_kv(flour_kv_cache* c, int layer, const void* k,
+                                       const void* v, int seq_len, int64_t stride_tok,
+                                       int64_t stride_head, void* stream) {
+    clear_error();
+    FLOUR_NEED(c, "kv_cache: null");
+    KvCacheImpl& x = c->c;
+    if (!x.device) {
+        set_error("kv_cache: write_kv needs a device pool (created with device_pool = 0)");
+        return FLOUR_ERR_UNSUPPORTED;
+    }
+    FLOUR_NEED(layer >= 0 && layer < x.num_layers, "kv_cache: layer %d of %d", layer,
+               x.num_layers);
+    FLOUR_NEED(seq_len >= 0 && seq_len <= x.table.len(),
+               "kv_cache: write of %d tokens, %d are live (allocate_kv first)", seq_len,
+               x.table.len());
+    if (seq_len == 0) return FLOUR_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = x.staging_ready();
+    if (rc) return rc;
+    const int end = x.table.len(), start = end - seq_len;
+    int32_t* slots = x.h_meta + x.num_blocks + 3;
+    for (int p = start; p < end; p++) slots[p - start] = (int32_t)x.table.slot(p);
+    rc = x.upload(x.num_blocks + 3, seq_len, s);
+    if (rc) return rc;
+    return flour_hip_kv_write(k, v, stride_tok, stride_head, x.k_pools[layer], x.v_pools[layer],
+                              x.d_slots(), seq_len, x.kv_heads, x.head_dim, x.num_slots, x.dtype,
+                              stream);
+}
+
+extern "C" int flour_kv_cache_attention(flour_kv_cache* c, int layer, const void* q,
+                                        int num_heads, int seq_q, int64_t q_stride_tok,
+                                        int64_t q_stride_head, void* out, int out_dtype,
+                                        int64_t o_stride_tok, int64_t o_stride_head, float scale,
+                                        void* stream) {
+    clear_error();
+    FLOUR_NEED(c, "kv_cache: null");
+    KvCacheImpl& x = c->c;
+    if (!x.device) {
+        set_error("kv_cache: attention needs a device pool (created with device_pool = 0)");
+        return FLOUR_ERR_UNSUPPORTED;
+    }
+    FLOUR_NEED(layer >= 0 && layer < x.num_layers, "kv_cache: layer %d of %d", layer,
+               x.num_layers);
+    FLOUR_NEED(num_heads > 0 && num_heads <= x.num_heads && num_heads % x.kv_heads == 0,
+               "kv_cache: %d query heads (cache built for up to %d, %d kv heads)", num_heads,
+               x.num_heads, x.kv_heads);
+    const int len = x.table.len();
+    FLOUR_NEED(seq_q >= 1 && seq_q <= len, "kv_cache: %d query rows over %d live positions",
+               seq_q, len);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int rc = x.upload_table(seq_q, s);
+    if (rc) return rc;
+    const int max_blocks = x.num_blocks;
+    if (seq_q == 1) {
+        FLOUR_NEED(q_stride_head == x.head_dim && o_stride_head == x.head_dim,
+                   "kv_cache: decode needs q and out as (num_heads, head_dim) contiguous");
+        return flour_hip_paged_decode(out, out_dtype, q, x.k_pools[layer], x.v_pools[layer],
+                                      x.d_table(), max_blocks, x.d_kv_len(), 1, num_heads,
+                                      x.kv_heads, x.head_dim, x.block_size, x.num_slots, len,
+                                      scale, x.dtype, x.d_ws, x.ws_bytes, stream);
+    }
+    return flour_hip_varlen_prefill(out, out_dtype, o_stride_tok, o_stride_head, q, q_stride_tok,
+                                    q_stride_head, x.k_pools[layer], x.v_pools[layer], x.d_cu(),
+                                    x.d_kv_len(), x.d_table(), max_blocks, 1, seq_q, seq_q,
+                                    num_heads, x.kv_heads, x.head_dim, x.block_size, x.num_slots,
+                                    scale, x.dtype, stream);
+}
+
+extern "C" int flour_kv_cache_reset_sequence(flour_kv_cache* c) {
+    clear_error();
+    FLOUR_NEED(c, "kv_cache: null");
+    c->c.reset_sequence();
+    return FLOUR_OK;
+}
+extern "C" int flour_kv_cache_match_prefix(flour_kv_cache* c, const uint32_t* tokens, int n) {
+    clear_error();
+    FLOUR_NEED(c && n >= 0 && (tokens || n == 0), "kv_cache: bad token list");
+    FLOUR_NEED(c->c.table.blocks().empty() && c->c.table.len() == 0,
+               "kv_cache: match_prefix needs a freshly reset sequence");
+    return c->c.match_prefix(tokens, n);
+}
+extern "C" int flour_kv_cache_register_prefix(flour_kv_cache* c, const uint32_t* tokens, int n) {
+    clear_error();
+    FLOUR_NEED(c && n >= 0 && (tokens || n == 0), "kv_cache: bad token list");
+    return c->c.register_prefix(tokens, n);
+}
+extern "C" int flour_kv_cache_clear_prefix_cache(flour_kv_cache* c) {
+    clear_error();
+    FLOUR_NEED(c, "kv_cache: null");
+    c->c.clear_prefix_cache();
+    return FLOUR_OK;
+}
+extern "C" int flour_kv_cache_pool(const flour_kv_cache* c, int layer, void** k_pool,
+                                   void** v_pool, int64_t* num_slots) {
+    clear_error();
+    FLOUR_NEED(c && k_pool && v_pool && num_slots, "kv_cache: bad arguments");
+    FLOUR_NEED(c->c.device, "kv_cache: no device pool");
+    FLOUR_NEED(layer >= 0 && layer < c->c.num_layers, "kv_cache: layer %d of %d", layer,
+               c->c.num_layers);
+    *k_pool = c->c.k_pools[layer];
+    *v_pool = c->c.v_pools[layer];
+    *num_slots = c->c.num_slots;
+    return FLOUR_OK;
+}

@@ -1,0 +1,251 @@
+"""Host-side KV cache over a device pool: the Python face of include/flour_cache.h.
+
+Mirrors the reference's per-sequence cache (src/models/common/cache.rs, paged.rs, prefix.rs)
+with the same method names and meaning:
+
+* ``BlockAllocator``  <- paged.rs:7-54   (LIFO free list, refcounts; allocate() -> id or None)
+* ``BlockTable``      <- paged.rs:57-121 (slot(pos) = blocks[pos // bs] * bs + pos % bs)
+* ``KvCache``         <- cache.rs KvCache + Cache: allocate_kv, write_kv, attention
+  (= kv_blocks + paged_attention), reset_sequence, match_prefix, register_prefix,
+  clear_prefix_cache, free_blocks, with the per-layer pools of PagedKvPool::new on the device.
+
+Every operation is one call into libflour_hip.so; errors raise ``FlourError`` with the
+library's message (the reference's ``candle_core::Error::Msg``).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+
+
+def _i32(n: int):
+    return (ctypes.c_int32 * max(n, 1))()
+
+
+def _tokens(tokens) -> tuple:
+    arr = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+    return arr, arr.ctypes.data_as(ctypes.c_void_p), int(arr.size)
+
+
+class BlockAllocator:
+    def __init__(self, num_blocks: int):
+        self._h = ctypes.c_void_p()
+        check(lib().flour_block_allocator_create(num_blocks, ctypes.byref(self._h)))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().flour_block_allocator_destroy(self._h)
+            self._h = None
+
+    def allocate(self):
+        i = lib().flour_block_allocator_allocate(self._h)
+        return None if i < 0 else i
+
+    def incref(self, block_id: int) -> None:
+        check(lib().flour_block_allocator_incref(self._h, block_id))
+
+    def decref(self, block_id: int) -> bool:
+        r = lib().flour_block_allocator_decref(self._h, block_id)
+        if r < 0:
+            check(r)
+        return bool(r)
+
+    def ref_count(self, block_id: int) -> int:
+        r = lib().flour_block_allocator_ref_count(self._h, block_id)
+        if r < 0:
+            check(r)
+        return r
+
+    def num_free(self) -> int:
+        return lib().flour_block_allocator_num_free(self._h)
+
+
+class BlockTable:
+    def __init__(self, block_size: int):
+        self._h = ctypes.c_void_p()
+        check(lib().flour_block_table_create(block_size, ctypes.byref(self._h)))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().flour_block_table_destroy(self._h)
+            self._h = None
+
+    def push_block(self, block_id: int) -> None:
+        check(lib().flour_block_table_push_block(self._h, block_id))
+
+    def advance(self, n: int) -> None:
+        check(lib().flour_block_table_advance(self._h, n))
+
+    def clear(self) -> None:
+        check(lib().flour_block_table_clear(self._h))
+
+    def len(self) -> int:
+        return lib().flour_block_table_len(self._h)
+
+    def is_empty(self) -> bool:
+        return self.len() == 0
+
+    def capacity(self) -> int:
+        return lib().flour_block_table_capacity(self._h)
+
+    def block_size(self) -> int:
+        return lib().flour_block_table_block_size(self._h)
+
+    def blocks(self) -> list[int]:
+        n = ctypes.c_int(0)
+        check(lib().flour_block_table_blocks(self._h, None, 0, ctypes.byref(n)))
+        out = _i32(n.value)
+        check(lib().flour_block_table_blocks(self._h, out, n.value, ctypes.byref(n)))
+        return list(out[: n.value])
+
+    def block_at(self, i: int) -> int:
+        return self.blocks()[i]
+
+    def slot(self, pos: int) -> int:
+        r = lib().flour_block_table_slot(self._h, pos)
+        if r < 0:
+            check(int(r))
+        return int(r)
+
+    def slots(self, start: int, end: int) -> list[int]:
+        out = _i32(end - start)
+        check(lib().flour_block_table_slots(self._h, start, end, out))
+        return list(out[: end - start])
+
+
+class KvCache:
+    """One sequence's paged KV cache (the reference's Cache / KvCache pair).
+
+    ``device_pool=False`` keeps only the bookkeeping (tests without a GPU)."""
+
+    def __init__(self, num_layers: int, max_seq_len: int, num_heads: int, kv_heads: int,
+                 head_dim: int, dtype=None, block_size: int = 16, device_pool: bool = True):
+        import torch
+
+        dtype = dtype or torch.bfloat16
+        self.num_layers, self.max_seq_len = num_layers, max_seq_len
+        self.num_heads, self.kv_heads, self.head_dim = num_heads, kv_heads, head_dim
+        self.block_size, self.dtype = block_size, dtype
+        self._h = ctypes.c_void_p()
+        from .ops import dtype_code
+
+        check(lib().flour_kv_cache_create(num_layers, max_seq_len, num_heads, kv_heads, head_dim,
+                                          block_size, dtype_code(dtype), int(device_pool),
+                                          ctypes.byref(self._h)))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().flour_kv_cache_destroy(self._h)
+            self._h = None
+
+    # ---- bookkeeping (cache.rs)
+    def allocate_kv(self, seq_len: int) -> None:
+        check(lib().flour_kv_cache_allocate_kv(self._h, seq_len))
+
+    def len(self) -> int:
+        return lib().flour_kv_cache_len(self._h)
+
+    def capacity(self) -> int:
+        return lib().flour_kv_cache_capacity(self._h)
+
+    def free_blocks(self) -> int:
+        return lib().flour_kv_cache_free_blocks(self._h)
+
+    def ref_count(self, block_id: int) -> int:
+        r = lib().flour_kv_cache_ref_count(self._h, block_id)
+        if r < 0:
+            check(r)
+        return r
+
+    def blocks(self) -> list[int]:
+        n = ctypes.c_int(0)
+        check(lib().flour_kv_cache_blocks(self._h, None, 0, ctypes.byref(n)))
+        out = _i32(n.value)
+        check(lib().flour_kv_cache_blocks(self._h, out, n.value, ctypes.byref(n)))
+        return list(out[: n.value])
+
+    def slots(self, start: int, end: int) -> list[int]:
+        out = _i32(end - start)
+        check(lib().flour_kv_cache_slots(self._h, start, end, out))
+        return list(out[: end - start])
+
+    def reset_sequence(self) -> None:
+        check(lib().flour_kv_cache_reset_sequence(self._h))
+
+    def match_prefix(self, token_ids) -> int:
+        arr, ptr, n = _tokens(token_ids)
+        r = lib().flour_kv_cache_match_prefix(self._h, ptr, n)
+        if r < 0:
+            check(r)
+        return r
+
+    def register_prefix(self, token_ids) -> None:
+        arr, ptr, n = _tokens(token_ids)
+        check(lib().flour_kv_cache_register_prefix(self._h, ptr, n))
+
+    def clear_prefix_cache(self) -> None:
+        check(lib().flour_kv_cache_clear_prefix_cache(self._h))
+
+    # ---- device side
+    def pool(self, layer: int):
+        """(k_pool, v_pool) of a layer as torch views of shape (kv_heads, num_slots, head_dim)."""
+        import torch
+
+        k, v, ns = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int64()
+        check(lib().flour_kv_cache_pool(self._h, layer, ctypes.byref(k), ctypes.byref(v),
+                                        ctypes.byref(ns)))
+        n = self.kv_heads * ns.value * self.head_dim
+        return tuple(_device_view(p.value, n, self.dtype).view(self.kv_heads, ns.value,
+                                                                self.head_dim) for p in (k, v))
+
+    def write_kv(self, layer: int, k, v) -> None:
+        """Cache::write_kv: k, v of shape (1, kv_heads, seq, head_dim) (the reference layout)
+        or (seq, kv_heads, head_dim); the trailing seq live positions take them."""
+        from .ops import _ptr, _stream
+
+        if k.dim() == 4:
+            seq = k.shape[2]
+            st, sh = k.stride(2), k.stride(1)
+        else:
+            seq = k.shape[0]
+            st, sh = k.stride(0), k.stride(1)
+        assert k.stride() == v.stride() and k.dtype == v.dtype == self.dtype
+        check(lib().flour_kv_cache_write_kv(self._h, layer, _ptr(k), _ptr(v), seq, st, sh,
+                                            _stream()))
+
+    def attention(self, layer: int, q, scale: float, out=None, out_dtype=None):
+        """Cache::kv_blocks + paged_attention: q of shape (1, num_heads, seq_q, head_dim)
+        (post-RoPE) attends causally to every live position; returns the same shape."""
+        import torch
+        from .ops import _ptr, _stream, dtype_code
+
+        assert q.dim() == 4 and q.shape[0] == 1
+        H, S, D = q.shape[1], q.shape[2], q.shape[3]
+        out_dtype = out_dtype or q.dtype
+        if out is None:
+            out = torch.empty((1, H, S, D), dtype=out_dtype, device=q.device)
+        check(lib().flour_kv_cache_attention(self._h, layer, _ptr(q), H, S, q.stride(2),
+                                             q.stride(1), _ptr(out), dtype_code(out.dtype),
+                                             out.stride(2), out.stride(1), float(scale),
+                                             _stream()))
+        return out
+
+
+def _device_view(addr: int, numel: int, dtype):
+    """A torch tensor over device memory owned by the library (no copy, no ownership)."""
+    import torch
+
+    class _Holder:
+        pass
+
+    h = _Holder()
+    h.__cuda_array_interface__ = {
+        "shape": (numel,), "typestr": "<u2" if dtype in (torch.bfloat16, torch.float16) else "<f4",
+        "data": (addr, False), "version": 3, "strides": None,
+    }
+    t = torch.as_tensor(h, device="cuda")
+    return t.view(dtype)

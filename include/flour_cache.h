@@ -1,0 +1,132 @@
+/*
+ * flour_cache.h — host-side KV-cache bookkeeping over a device pool, the C-ABI of the layer
+ * that sits directly above the kernels of flour_hip.h in libflour_hip.so.
+ *
+ * It restates the reference's per-sequence cache (reference files cited as path:line,
+ * relative to the lltsdyp/flour checkout):
+ *
+ *   src/models/common/paged.rs:7-54     BlockAllocator (LIFO free list, per-block refcounts)
+ *   src/models/common/paged.rs:57-121   BlockTable (logical position -> physical slot)
+ *   src/models/common/prefix.rs:1-60    block_hash / PrefixRegistry (chained full-block hashes)
+ *   src/models/common/paged.rs:138-167  PagedKvPool::new (here: device arrays, zero-filled)
+ *   src/models/common/cache.rs:13-165   KvCache (allocate, write_current, gather_blocks,
+ *                                       reset_sequence, match_prefix, register_prefix)
+ *   src/models/common/cache.rs:429-505  Cache::allocate_kv / write_kv / kv_blocks / ...
+ *
+ * and replaces the `kv_blocks` + `paged_attention` pair of the attention layer
+ * (src/models/common/attention.rs:104-109) by one call that marshals the block table to the
+ * device and launches the decode (seq_q == 1) or prefill kernel.
+ *
+ * Conventions are those of flour_hip.h: FLOUR_OK or a negative FLOUR_ERR_* code, with the
+ * message in flour_hip_last_error(). Functions of one cache must not be called concurrently.
+ * Block ids and slots are int32 (the pool holds fewer than 2^31 slots).
+ */
+#ifndef FLOUR_CACHE_H
+#define FLOUR_CACHE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- BlockAllocator (paged.rs:7-54) --------------------------------------------------- */
+typedef struct flour_block_allocator flour_block_allocator;
+
+/* BlockAllocator::new: every block free; the first allocate returns block 0 (paged.rs:13-19). */
+int flour_block_allocator_create(int num_blocks, flour_block_allocator** out);
+void flour_block_allocator_destroy(flour_block_allocator* a);
+/* BlockAllocator::allocate: a block id with refcount 1, or -1 when none is free (None). */
+int flour_block_allocator_allocate(flour_block_allocator* a);
+/* BlockAllocator::incref. */
+int flour_block_allocator_incref(flour_block_allocator* a, int block_id);
+/* BlockAllocator::decref: 1 when the block reached zero references and was freed, else 0;
+ * FLOUR_ERR_INVALID_ARGUMENT for an unreferenced or unknown block (a debug_assert there). */
+int flour_block_allocator_decref(flour_block_allocator* a, int block_id);
+int flour_block_allocator_ref_count(const flour_block_allocator* a, int block_id);
+int flour_block_allocator_num_free(const flour_block_allocator* a);
+
+/* ---- BlockTable (paged.rs:57-121) ----------------------------------------------------- */
+typedef struct flour_block_table flour_block_table;
+
+int flour_block_table_create(int block_size, flour_block_table** out);
+void flour_block_table_destroy(flour_block_table* t);
+int flour_block_table_push_block(flour_block_table* t, int block_id);
+int flour_block_table_advance(flour_block_table* t, int n);
+int flour_block_table_clear(flour_block_table* t);
+int flour_block_table_len(const flour_block_table* t);
+int flour_block_table_capacity(const flour_block_table* t);
+int flour_block_table_block_size(const flour_block_table* t);
+/* BlockTable::blocks: copies up to `cap` ids to `out`, stores the count in *n. */
+int flour_block_table_blocks(const flour_block_table* t, int32_t* out, int cap, int* n);
+/* BlockTable::slot / slots(start, end): blocks[pos / bs] * bs + pos % bs. Positions must be
+ * backed by a pushed block. */
+int64_t flour_block_table_slot(const flour_block_table* t, int pos);
+int flour_block_table_slots(const flour_block_table* t, int start, int end, int32_t* out);
+
+/* ---- KvCache + Cache (cache.rs) -------------------------------------------------------- */
+typedef struct flour_kv_cache flour_kv_cache;
+
+/* KvCache::new (cache.rs:21-41): ceil(max_seq_len / block_size) blocks. With device_pool != 0
+ * the per-layer K and V pools (kv_heads, num_slots, head_dim) are allocated zero-filled on the
+ * current HIP device, together with the small device buffers the kernels read (block table,
+ * slot mapping, lengths, decode workspace for up to num_heads query heads); with
+ * device_pool == 0 only the bookkeeping exists (write_kv / attention then fail). */
+int flour_kv_cache_create(int num_layers, int max_seq_len, int num_heads, int kv_heads,
+                          int head_dim, int block_size, int dtype, int device_pool,
+                          flour_kv_cache** out);
+void flour_kv_cache_destroy(flour_kv_cache* c);
+
+/* Cache::allocate_kv (cache.rs:429-447): reserve blocks for seq_len more tokens and advance
+ * the live length. Errors: "paged kv cache overflow" past max_seq_len (FLOUR_ERR_CAPACITY),
+ * "out of kv blocks" (FLOUR_ERR_OUT_OF_BLOCKS). */
+int flour_kv_cache_allocate_kv(flour_kv_cache* c, int seq_len);
+int flour_kv_cache_len(const flour_kv_cache* c);
+int flour_kv_cache_capacity(const flour_kv_cache* c);
+/* KvCache::free_blocks (cache.rs:361-363). */
+int flour_kv_cache_free_blocks(const flour_kv_cache* c);
+int flour_kv_cache_ref_count(const flour_kv_cache* c, int block_id);
+/* The live block table (BlockTable::blocks) and KvCache::slots(start, end). */
+int flour_kv_cache_blocks(const flour_kv_cache* c, int32_t* out, int cap, int* n);
+int flour_kv_cache_slots(const flour_kv_cache* c, int start, int end, int32_t* out);
+
+/* Cache::write_kv -> KvCache::write_current (cache.rs:71-77): the trailing seq_len tokens of
+ * the live sequence take k/v element (t, h, d) at t*stride_tok + h*stride_head + d
+ * (device memory; the reference's (1, kv_heads, seq, head_dim) is stride_tok = head_dim,
+ * stride_head = seq_len * head_dim). Launches flour_hip_kv_write on `stream`. */
+int flour_kv_cache_write_kv(flour_kv_cache* c, int layer, const void* k, const void* v,
+                            int seq_len, int64_t stride_tok, int64_t stride_head, void* stream);
+
+/* Cache::kv_blocks + paged_attention (cache.rs:456-458, cpu.rs:57-112) in one call: the
+ * last seq_q rows of the live sequence attend causally to all live positions. q element
+ * (row, head, d) at row*q_stride_tok + head*q_stride_head + d, out likewise with the o_
+ * strides ((1, num_heads, seq_q, head_dim) is stride_tok = head_dim, stride_head =
+ * seq_q * head_dim). seq_q == 1 runs the decode kernel, which requires out to be
+ * (num_heads, head_dim) contiguous. The block table is copied to the device on `stream` when
+ * it changed since the last call. */
+int flour_kv_cache_attention(flour_kv_cache* c, int layer, const void* q, int num_heads,
+                             int seq_q, int64_t q_stride_tok, int64_t q_stride_head, void* out,
+                             int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,
+                             float scale, void* stream);
+
+/* KvCache::reset_sequence (cache.rs:100-108). */
+int flour_kv_cache_reset_sequence(flour_kv_cache* c);
+/* KvCache::match_prefix (cache.rs:112-143): tokens served from cached full blocks (a multiple
+ * of block_size; never the whole prompt). */
+int flour_kv_cache_match_prefix(flour_kv_cache* c, const uint32_t* tokens, int n);
+/* KvCache::register_prefix (cache.rs:145-159). */
+int flour_kv_cache_register_prefix(flour_kv_cache* c, const uint32_t* tokens, int n);
+/* KvCache::clear_prefix_cache (cache.rs:354-359). */
+int flour_kv_cache_clear_prefix_cache(flour_kv_cache* c);
+
+/* Device pools of one layer (PagedKvPool::block_view, paged.rs:266-279: slot s of kv head h is
+ * row h * num_slots + s of each array). */
+int flour_kv_cache_pool(const flour_kv_cache* c, int layer, void** k_pool, void** v_pool,
+                        int64_t* num_slots);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLOUR_CACHE_H */
