@@ -225,26 +225,28 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     f32x16 st[2];
     auto visible = [&](int kt) { return wave_active && kt * PF_KT <= wave_lim; };  // per wave
     auto qk = [&](int kbuf) __attribute__((always_inline)) {
-        // ---- S^T tile (64 tokens x 32 queries) in two 32-token halves, raw q.k
+        // ---- S^T tile (64 tokens x 32 queries) in two 32-token halves, raw q.k. Issue order,
+        // pinned with scheduling fences: the first half's eight K reads, then each product of
+        // the first half followed by one K read of the second half, then the second half's
+        // products (every read is in flight for at least one product).
+        const uint16_t* kr0 = &Ks[kbuf][ql32 * PF_KPITCH + 8 * h2];
+        const uint16_t* kr1 = kr0 + 32 * PF_KPITCH;
+        u32x4 a0[8], a1[8];
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
+        for (int kk = 0; kk < 8; kk++) a0[kk] = *reinterpret_cast<const u32x4*>(kr0 + 16 * kk);
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int y = 0; y < 16; y++) st[mt][y] = 0.0f;
-            const uint16_t* kr = &Ks[kbuf][(32 * mt + ql32) * PF_KPITCH + 8 * h2];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int kk = 0; kk < 8; kk++) {
-                const u32x4 a = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
-                st[mt] = mfma32x32x16<T>(a, qb[kk], st[mt]);
-            }
+        for (int kk = 0; kk < 8; kk++) {
+            st[0] = mfma32x32x16<T>(a0[kk], qb[kk], st[0]);
+            a1[kk] = *reinterpret_cast<const u32x4*>(kr1 + 16 * kk);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // issue order: the first half's K reads, then each product followed by one read of
-        // the second half's K
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
+        for (int kk = 0; kk < 8; kk++) st[1] = mfma32x32x16<T>(a1[kk], qb[kk], st[1]);
     };
     auto sm_pv = [&](int kt, int vbuf) __attribute__((always_inline)) {
         const int kv0 = kt * PF_KT;
@@ -286,58 +288,48 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         const float nm = -m;
         u32x4 pb_hi[4], pb_lo[4];
         float psum = 0.0f;
-        auto weights = [&](int kk2) __attribute__((always_inline)) {
+        // weights of step kk2, rows 2x and 2x+1 of the P^T B operand
+        auto weight = [&](int kk2, int x) __attribute__((always_inline)) {
             const int mt = kk2 >> 1, y0 = 8 * (kk2 & 1);
-#pragma unroll
-            for (int x = 0; x < 4; x++) {
-                const float a0 = fast_exp2(fmaf(st[mt][y0 + 2 * x], scale_log2, nm));
-                const float a1 = fast_exp2(fmaf(st[mt][y0 + 2 * x + 1], scale_log2, nm));
-                const uint32_t hi = pack2<TV>(a0, a1);
-                pb_hi[kk2][x] = hi;
-                if constexpr (PV == PV_HILO) {
-                    pb_lo[kk2][x] = pack2<TV>(a0 - lo_f32<TV>(hi), a1 - hi_f32<TV>(hi));
-                    psum += a0 + a1;
-                } else {
-                    psum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, hi), f16x2{1, 1}, psum,
-                                                  false);
-                }
+            const float a0 = fast_exp2(fmaf(st[mt][y0 + 2 * x], scale_log2, nm));
+            const float a1 = fast_exp2(fmaf(st[mt][y0 + 2 * x + 1], scale_log2, nm));
+            const uint32_t hi = pack2<TV>(a0, a1);
+            pb_hi[kk2][x] = hi;
+            if constexpr (PV == PV_HILO) {
+                pb_lo[kk2][x] = pack2<TV>(a0 - lo_f32<TV>(hi), a1 - hi_f32<TV>(hi));
+                psum += a0 + a1;
+            } else {
+                psum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, hi), f16x2{1, 1}, psum,
+                                              false);
             }
         };
+        // Issue order, pinned with scheduling fences: the V reads and weights of step 0, then
+        // each product of step kk2 followed by one V read and a quarter of the weights of
+        // step kk2 + 1.
         const uint16_t* vr = &Vt[vbuf][ql32 * PF_VPITCH + 8 * h2];
         u32x4 vf[2][4];
 #pragma unroll
         for (int mt2 = 0; mt2 < 4; mt2++)
             vf[0][mt2] = *reinterpret_cast<const u32x4*>(vr + 32 * mt2 * PF_VPITCH);
-        weights(0);
+#pragma unroll
+        for (int x = 0; x < 4; x++) weight(0, x);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk2 = 0; kk2 < 4; kk2++) {
-            if (kk2 < 3) {
-#pragma unroll
-                for (int mt2 = 0; mt2 < 4; mt2++)
-                    vf[(kk2 + 1) & 1][mt2] = *reinterpret_cast<const u32x4*>(
-                        vr + 32 * mt2 * PF_VPITCH + 16 * (kk2 + 1));
-                weights(kk2 + 1);
-            }
 #pragma unroll
             for (int mt2 = 0; mt2 < 4; mt2++) {
                 o[mt2] = mfma32x32x16<TV>(vf[kk2 & 1][mt2], pb_hi[kk2], o[mt2]);
                 if constexpr (PV == PV_HILO)
                     o[mt2] = mfma32x32x16<TV>(vf[kk2 & 1][mt2], pb_lo[kk2], o[mt2]);
+                if (kk2 < 3) {
+                    vf[(kk2 + 1) & 1][mt2] = *reinterpret_cast<const u32x4*>(
+                        vr + 32 * mt2 * PF_VPITCH + 16 * (kk2 + 1));
+                    weight(kk2 + 1, mt2);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         lsum += psum;
-        if constexpr (PV == PV_F16) {
-            // issue order: V reads and weights of step 0, then each product followed by a
-            // share of the next step's VALU work and one V read
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x402, 24, 0);
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                if (i < 12) __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
-            }
-        }
     };
 
     // ---- pipeline: one barrier per tile; global loads run two tiles ahead of the compute
@@ -349,6 +341,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     page_bases(min(1, n_kt - 1), pb1);
     gload(1, pb1, 1 < n_kt, kb, vb);
     page_bases(min(2, n_kt - 1), pb2);
+    // Q must have landed before the loop (its loads precede the tile loads, so this waits for
+    // them alone); otherwise the compiler sinks the Q loads past the first barrier and keeps a
+    // conservative wait for them inside the loop
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) asm volatile("" ::"v"(qb[kk]));
     lds_store(0, ka, va);
     __syncthreads();
     // step kt: refill `nx` with tile kt + 2, compute tile kt, store tile kt + 1 (held in `st1`)
