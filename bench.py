@@ -43,6 +43,9 @@ def parse_args():
     ap.add_argument("--workload", default="decode_bf16_llama3_8b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the decode step from a HIP graph instead of launching it eagerly "
+                         "(measured slower than eager launches for this two-kernel step)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -171,7 +174,10 @@ def cpu_prefill_baseline(case, seconds: float):
     return flops / med / 1e12, threads, len(times), S, P
 
 
-def bench_decode(torch, ops, case, steps, warmup):
+def bench_decode(torch, ops, case, steps, warmup, graph: bool = False):
+    """Times decode steps. With graph=True the step (main + merge kernel) is captured once in a
+    HIP graph and replayed, as a serving loop would, which removes the host launch overhead;
+    the kernels and their arguments are the same as in the eager call."""
     ws = ops.DecodeWorkspace(case.q.device)
     out = torch.empty_like(case.q)
 
@@ -180,7 +186,19 @@ def bench_decode(torch, ops, case, steps, warmup):
                          case.scale, case.max_context_len, block_size=case.block_size, out=out,
                          workspace=ws)
 
-    wall_ms, per = event_timed(torch, step, steps, warmup)
+    run = step
+    if graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()  # sizes the workspace before capture
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        run = g.replay
+    wall_ms, per = event_timed(torch, run, steps, warmup)
     kern_ms = sum(per) / len(per)
     nbytes = case.algorithmic_bytes()
     return dict(ms_per_step=wall_ms, kernel_ms=kern_ms, bytes=nbytes,
@@ -269,7 +287,7 @@ def main():
     if cfg["kind"] != "decode":
         print(json.dumps(prefill_line(torch, ops, case, name, cfg, args)), flush=True)
         return
-    r = bench_decode(torch, ops, case, args.steps, args.warmup)
+    r = bench_decode(torch, ops, case, args.steps, args.warmup, graph=args.graph)
     value = r["gbs_step"]
 
     result = {
@@ -291,6 +309,7 @@ def main():
             "block_size": cfg["block_size"], "context_lens": f"U[{cfg['ctx'][0]},{cfg['ctx'][1]}]",
             "total_context_tokens": int(case.context_lens.sum().item()),
             "algorithmic_bytes_per_step": r["bytes"], "out_dtype": "bf16",
+            "launch": "HIP graph replay of the step" if args.graph else "eager",
         },
         "roofline": {
             "bound": "hbm", "kernel": "paged_decode_mfma_kernel + paged_decode_merge_kernel",
