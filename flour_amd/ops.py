@@ -137,6 +137,37 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     return out
 
 
+def prepare_paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                         block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                         max_context_len: int, out: torch.Tensor, workspace: DecodeWorkspace,
+                         block_size: int = 16):
+    """Validates the arguments of paged_decode once and returns a callable that relaunches the
+    same decode step (same tensors, current stream at preparation time) with no per-call
+    Python work beyond the C call, as a serving loop that reuses its buffers would."""
+    _need_cuda(q, k_pool, v_pool, block_tables, context_lens, out)
+    _need_i32(block_tables, context_lens)
+    B, H, D = q.shape
+    G, num_slots, Dk = k_pool.shape
+    if Dk != D or not q.is_contiguous() or not k_pool.is_contiguous() or not v_pool.is_contiguous():
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT, "q and pools must be contiguous with matching head_dim")
+    if q.dtype != k_pool.dtype or out.shape != q.shape or not out.is_contiguous():
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT, "q, pools and out must agree")
+    _check_block_size(num_slots, block_size)
+    ws = workspace.get(decode_workspace_bytes(B, H, G, D, max_context_len))
+    args = (_ptr(out), dtype_code(out.dtype), _ptr(q), _ptr(k_pool), _ptr(v_pool),
+            _ptr(block_tables), block_tables.shape[1], _ptr(context_lens), B, H, G, D,
+            block_size, num_slots, max_context_len, float(scale), dtype_code(q.dtype), _ptr(ws),
+            ws.numel(), _stream())
+    fn = lib().flour_hip_paged_decode
+
+    def run() -> None:
+        rc = fn(*args)
+        if rc:
+            check(rc)
+
+    return run
+
+
 def varlen_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                    cu_seqlens_q: torch.Tensor, kv_lens: torch.Tensor, block_tables: torch.Tensor,
                    max_seqlen_q: int, scale: float, block_size: int = 16,
