@@ -202,3 +202,16 @@ def test_decode_graph_replay_matches_eager(device):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs"
         assert torch.isfinite(noise)
+
+
+def test_decode_batch_beyond_the_mfma_limit_uses_the_generic_kernel(device):
+    """5000 sequences (past the 4096-sequence bound of the MFMA decode) still decode correctly
+    on the generic kernel; short contexts keep the oracle fast."""
+    d = make_decode(5000, 8, 2, 128, 16, (1, 40), dtype=torch.bfloat16, seed=3, device=device)
+    out = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens, d.scale,
+                           d.max_context_len, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.paged_attention(to_np(d.q), to_np(d.k_pool), to_np(d.v_pool), to_np(d.block_tables),
+                            np.arange(5001, dtype=np.int32), to_np(d.context_lens), 16, d.scale)
+    max_abs, rel = errors(to_np(out), ref)
+    assert max_abs <= 2e-3 and rel <= 1e-3, (max_abs, rel)

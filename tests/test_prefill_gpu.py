@@ -150,3 +150,43 @@ def test_prefill_hilo_mode_meets_the_same_bounds(device):
     max_abs, rel = errors(got, ref)
     print(f"hi+lo P: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_prefill_bf16_mfma_larger_blocks(device, bs):
+    """The MFMA path with pages of 32 / 64 tokens (a 64-token tile spans one or two pages)."""
+    c = make_prefill(3, 16, 4, 128, bs, (1, 1), prefix=2 * bs, dtype=torch.bfloat16, seed=bs,
+                     device=device, q_lens=[70, 1, 200])
+    write(c)
+    check_bf16(c, tag=f"bs={bs}")
+
+
+def test_prefill_f16_pools(device):
+    """fp16 storage on the MFMA path (Q.K in fp16, P.V in fp16)."""
+    c = make_prefill(2, 8, 2, 128, 16, (1, 1), prefix=32, dtype=torch.float16, seed=21,
+                     device=device, q_lens=[90, 33])
+    write(c)
+    ref, rows = oracle_prefill(c)
+    got = to_np(run(c, torch.float32))[rows]
+    max_abs, rel = errors(got, ref)
+    print(f"f16 fp32-out max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+def test_prefill_long_sequence_many_tiles(device):
+    """One 4100-row sequence (33 query tiles, 65 kv tiles for the last) next to a 1-row one;
+    the oracle checks the first and last rows of the long sequence and the short one."""
+    c = make_prefill(2, 8, 2, 128, 16, (1, 1), prefix=0, dtype=torch.bfloat16, seed=31,
+                     device=device, q_lens=[4100, 1])
+    write(c)
+    out = to_np(run(c, torch.float32))
+    cu = to_np(c.cu_seqlens_q)
+    # rows of the long sequence: the oracle runs on the whole sequence, compare a sample
+    ref, rows = oracle_prefill(c, seqs=[0])
+    pick = np.r_[0:64, 2000:2064, 4036:4100]
+    max_abs, rel = errors(out[rows][pick], ref[pick])
+    print(f"long fp32-out max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+    ref1, rows1 = oracle_prefill(c, seqs=[1])
+    assert errors(out[rows1], ref1)[0] <= 2e-3
+    assert cu[-1] == 4101
