@@ -33,6 +33,7 @@
 //    significant bits).
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "flour_common.h"
@@ -55,6 +56,10 @@ static constexpr float PF_RESCALE_SLACK = 8.0f;  // log2 units the reference max
 static constexpr int PF_KPITCH = PF_D + 8;   // elements: 272 B rows
 static constexpr int PF_VPITCH = PF_KT + 8;  // elements: 144 B rows
 static constexpr float PF_LOG2E = 1.4426950408889634f;
+// Persistent schedule limits (the per-workgroup item table lives in LDS); larger batches use
+// one workgroup per item.
+static constexpr int PF_MAX_SEQS = 2048;
+static constexpr int PF_MAX_LEVELS = 512;  // query tiles per sequence (65536 rows)
 
 __device__ __forceinline__ int swap_bits01(int x) {
     return (x & ~3) | ((x & 1) << 1) | ((x >> 1) & 1);
@@ -80,27 +85,133 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int64_t q_sh, const T* __restrict__ k_pool, const T* __restrict__ v_pool,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ block_tables, int max_blocks, int num_seqs, int num_heads,
-    int n_rep, int block_size, int64_t num_slots, int n_qt_max, float scale_log2) {
+    int n_rep, int block_size, int64_t num_slots, int n_qt_max, int persistent,
+    float scale_log2) {
     constexpr int D = PF_D;
     // V^T is staged as fp16 for PV_F16, as the storage type otherwise; K keeps the storage type.
     typedef typename std::conditional<PV == PV_F16, f16_t, T>::type TV;
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][PF_KT * PF_KPITCH];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][PF_D * PF_VPITCH];
 
-    // ---- work item: (query tile, sequence, pair of query heads). Workgroups are issued in
-    // decreasing query-tile index: the cost of a tile grows with its index (its causal kv range
-    // is kv_len - q_len + 128 (qt + 1)), so this is close to longest-first order, and every
-    // tile level is spread over all XCDs (the dispatcher deals workgroups to the 8 XCDs
-    // round-robin). Items past a sequence's last tile exit at once.
+    // ---- work items: (query tile, sequence, pair of query heads), ordered by decreasing
+    // query-tile index ("level"): the cost of an item grows with its tile index (its causal kv
+    // range is kv_len - q_len + 128 (qt + 1)), so this is close to longest-first order.
+    //  * persistent: one workgroup per CU walks the items that exist (sequences too short for
+    //    a level are left out), item k*G + b on even rounds k and k*G + G-1-b on odd ones
+    //    (a snake over the longest-first list balances the workgroups without shared state);
+    //  * otherwise: one workgroup per (level, sequence, pair), items past a sequence's last
+    //    tile exit at once, and the dispatcher deals the levels over all XCDs.
     const int pairs_per_kv = (n_rep + 1) >> 1;
     const int kv_heads = num_heads / n_rep;
     const int npairs = kv_heads * pairs_per_kv;
-    const int per_rank = num_seqs * npairs;
-    const int bid = blockIdx.x;
-    const int level = bid / per_rank;
-    const int r = bid - level * per_rank;
-    const int seq = r / npairs;
-    const int hp = r - seq * npairs;
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int h2 = lane >> 5, ql32 = lane & 31;
+    const int NQ = n_qt_max;
+
+    __shared__ int sched_order[PF_MAX_SEQS];       // sequences by decreasing tile count
+    __shared__ int sched_more[PF_MAX_LEVELS + 1];  // [v]: sequences with more than v tiles
+    __shared__ int sched_fill[PF_MAX_LEVELS + 1];
+    __shared__ int sched_cum[PF_MAX_LEVELS + 2];   // [L]: items before level L
+    auto seq_tiles = [&](int sq) {  // query tiles of a sequence (0 if it cannot be served)
+        const int l = cu_seqlens[sq + 1] - cu_seqlens[sq];
+        const int kl = min(kv_lens[sq], max_blocks * block_size);
+        return (l <= 0 || kl < l) ? 0 : min((l + PF_QT - 1) / PF_QT, NQ);
+    };
+    // exclusive suffix / prefix scans over up to PF_MAX_LEVELS + 1 entries by wave 0
+    auto wave_scan = [&](int n, auto&& get, auto&& put, bool suffix) {
+        const int per = (n + 63) / 64;
+        int local = 0;
+        for (int i = 0; i < per; i++) {
+            const int x = lane * per + i;
+            if (x < n) local += get(suffix ? n - 1 - x : x);
+        }
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        int run = incl - local;
+        for (int i = 0; i < per; i++) {
+            const int x = lane * per + i;
+            if (x < n) {
+                const int v = get(suffix ? n - 1 - x : x);
+                put(suffix ? n - 1 - x : x, run);
+                run += v;
+            }
+        }
+        return __shfl(incl, 63, 64);  // total
+    };
+    int total_items = 0;
+    if (persistent) {
+        for (int v = tid; v <= NQ; v += PF_THREADS) sched_fill[v] = 0;
+        __syncthreads();
+        for (int sq = tid; sq < num_seqs; sq += PF_THREADS) atomicAdd(&sched_fill[seq_tiles(sq)], 1);
+        __syncthreads();
+        if (w == 0) {
+            // more[v] = sequences with a tile count above v (a suffix sum of the histogram)
+            wave_scan(NQ + 1, [&](int v) { return sched_fill[v]; },
+                      [&](int v, int x) { sched_more[v] = x; }, true);
+        }
+        __syncthreads();
+        for (int v = tid; v <= NQ; v += PF_THREADS) sched_fill[v] = 0;
+        __syncthreads();
+        if (w == 0) {
+            // stable counting sort (every workgroup must build the same order): 64 sequences
+            // at a time, a lane's rank among equal tile counts comes from ballots over the
+            // count's bits (counts are at most PF_MAX_LEVELS < 1024)
+            for (int base = 0; base < num_seqs; base += 64) {
+                const int sq = base + lane;
+                const int n = sq < num_seqs ? seq_tiles(sq) : 0;
+                uint64_t same = ~0ull;
+#pragma unroll
+                for (int b = 0; b < 10; b++) {
+                    const uint64_t bal = __ballot((n >> b) & 1);
+                    same &= ((n >> b) & 1) ? bal : ~bal;
+                }
+                const int rank = __popcll(same & ((1ull << lane) - 1));
+                const int fill = sched_fill[n];
+                if (n > 0) sched_order[sched_more[n] + fill + rank] = sq;
+                if (rank == 0) sched_fill[n] = fill + __popcll(same);
+            }
+        }
+        __syncthreads();
+        if (w == 0) {
+            // level L (tile qt = NQ-1-L) holds one item per pair of every sequence with more
+            // than qt tiles
+            const int t = wave_scan(NQ, [&](int L) { return npairs * sched_more[NQ - 1 - L]; },
+                                    [&](int L, int x) { sched_cum[L] = x; }, false);
+            if (lane == 0) sched_cum[NQ] = t;
+        }
+        __syncthreads();
+        total_items = sched_cum[NQ];
+    }
+    const int G = gridDim.x;
+    int level_hint = 0;
+    for (int round = 0;; round++) {
+        int level, seq, hp;
+        if (persistent) {
+            const int item = round * G + ((round & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x);
+            if (item >= total_items) break;
+            while (sched_cum[level_hint + 1] <= item) level_hint++;  // items only grow
+            level = level_hint;
+            const int j = item - sched_cum[level];
+            seq = sched_order[j / npairs];
+            hp = j - (j / npairs) * npairs;
+        } else {
+            if (round > 0) break;
+            const int per_rank = num_seqs * npairs;
+            const int bid = blockIdx.x;
+            level = bid / per_rank;
+            const int r = bid - level * per_rank;
+            seq = r / npairs;
+            hp = r - seq * npairs;
+        }
+        level = __builtin_amdgcn_readfirstlane(level);
+        seq = __builtin_amdgcn_readfirstlane(seq);
+        hp = __builtin_amdgcn_readfirstlane(hp);
     const int kvh = hp / pairs_per_kv;
     const int hj = hp - kvh * pairs_per_kv;
 
@@ -110,17 +221,13 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // past the table).
     const int kv_len = min(kv_lens[seq], max_blocks * block_size);
     const int qt = n_qt_max - 1 - level;
-    if (qt * PF_QT >= ql || kv_len < ql) return;
+    if (qt * PF_QT >= ql || kv_len < ql) continue;
     const int off = kv_len - ql;
     const int row_begin = qt * PF_QT;
     const int row_last = min(row_begin + PF_QT, ql) - 1;
     const int kv_end = off + row_last + 1;  // exclusive bound of visible kv for this tile
     const int n_kt = (kv_end + PF_KT - 1) / PF_KT;
 
-    const int tid = threadIdx.x;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-    const int h2 = lane >> 5, ql32 = lane & 31;
     const int hsel = w >> 2;  // which head of the pair
     const int head = kvh * n_rep + 2 * hj + hsel;
     const bool head_ok = 2 * hj + hsel < n_rep;
@@ -373,22 +480,41 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // ---- epilogue: lane (h2, q) holds dims 32 mt2 + 8 i + 4 h2 + j of query row wr0 + q
     lsum += wave_shfl_xor(lsum, 32);
     const int orow = wr0 + ql32;
-    if (!wave_active || orow >= ql) return;
-    const float inv = 1.0f / lsum;
-    TO* op = out + (int64_t)(q0 + orow) * o_st + (int64_t)head * o_sh + 4 * h2;
+    if (wave_active && orow < ql) {
+        const float inv = 1.0f / lsum;
+        TO* op = out + (int64_t)(q0 + orow) * o_st + (int64_t)head * o_sh + 4 * h2;
 #pragma unroll
-    for (int mt2 = 0; mt2 < 4; mt2++)
+        for (int mt2 = 0; mt2 < 4; mt2++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            TO* dst = op + 32 * mt2 + 8 * i;
-            const float a0 = o[mt2][4 * i] * inv, a1 = o[mt2][4 * i + 1] * inv;
-            const float a2 = o[mt2][4 * i + 2] * inv, a3 = o[mt2][4 * i + 3] * inv;
-            if constexpr (sizeof(TO) == 4) {
-                *reinterpret_cast<f32x4*>(dst) = f32x4{a0, a1, a2, a3};
-            } else {
-                *reinterpret_cast<u32x2*>(dst) = u32x2{pack2<TO>(a0, a1), pack2<TO>(a2, a3)};
+            for (int i = 0; i < 4; i++) {
+                TO* dst = op + 32 * mt2 + 8 * i;
+                const float a0 = o[mt2][4 * i] * inv, a1 = o[mt2][4 * i + 1] * inv;
+                const float a2 = o[mt2][4 * i + 2] * inv, a3 = o[mt2][4 * i + 3] * inv;
+                if constexpr (sizeof(TO) == 4) {
+                    *reinterpret_cast<f32x4*>(dst) = f32x4{a0, a1, a2, a3};
+                } else {
+                    *reinterpret_cast<u32x2*>(dst) =
+                        u32x2{pack2<TO>(a0, a1), pack2<TO>(a2, a3)};
+                }
             }
-        }
+    }
+    }  // items
+}
+
+static int g_prefill_persistent = 1;  // a tuning / test switch
+
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
 }
 
 template <typename T, typename TO, int PV>
@@ -399,7 +525,10 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
                                int n_rep, int block_size, int64_t num_slots, float scale,
                                hipStream_t stream) {
     const int64_t n_qt = (max_seqlen_q + PF_QT - 1) / PF_QT;
-    const int64_t grid = n_qt * num_seqs * (num_heads / n_rep) * ((n_rep + 1) / 2);
+    const int64_t items = n_qt * num_seqs * (num_heads / n_rep) * ((n_rep + 1) / 2);
+    const bool persistent = g_prefill_persistent && num_seqs <= PF_MAX_SEQS &&
+                            n_qt <= PF_MAX_LEVELS;
+    const int64_t grid = persistent ? std::min<int64_t>(items, device_cus()) : items;
     if (grid > 0x7fffffff) {
         set_error("varlen_prefill: grid too large");
         return FLOUR_ERR_UNSUPPORTED;
@@ -410,7 +539,8 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
     kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
         static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
         static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt, max_blocks,
-        num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt, scale * PF_LOG2E);
+        num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt, (int)persistent,
+        scale * PF_LOG2E);
     return check_hip(hipGetLastError(), "varlen_prefill launch");
 }
 
@@ -420,6 +550,11 @@ static int g_prefill_pv_mode = PV_F16;
 }  // namespace flour
 
 using namespace flour;
+
+extern "C" int flour_hip_set_prefill_persistent(int on) {
+    g_prefill_persistent = on ? 1 : 0;
+    return FLOUR_OK;
+}
 
 extern "C" int flour_hip_set_prefill_precise_p(int on) {
     g_prefill_pv_mode = on ? PV_HILO : PV_F16;

@@ -190,3 +190,43 @@ def test_prefill_long_sequence_many_tiles(device):
     ref1, rows1 = oracle_prefill(c, seqs=[1])
     assert errors(out[rows1], ref1)[0] <= 2e-3
     assert cu[-1] == 4101
+
+
+@pytest.mark.parametrize("H,G", [(12, 4), (8, 8)])
+def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G):
+    """The persistent schedule (one workgroup per CU walking the longest-first list of query
+    tiles) gives bit-identical output to one workgroup per (tile, sequence, head pair), with
+    empty sequences, a sequence whose kv length is below its query length (skipped: its rows
+    stay untouched) and an odd GQA group (a pair with one idle head)."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(3)
+    lens = [int(x) for x in rng.integers(0, 700, size=37)]
+    lens[5] = 0
+    lens[11] = 1
+    lens[20] = 690
+    lens[7] = 50
+    c = make_prefill(len(lens), H, G, 128, 16, (1, 1), prefix=32, dtype=torch.bfloat16, seed=9,
+                     device=device, q_lens=lens)
+    write(c)
+    c.kv_lens[7] = 49  # kv_len < q_len: the sequence is skipped
+
+    def go(persistent):
+        out = torch.full((c.q.shape[0], H, 128), 7.0, dtype=torch.float32, device=device)
+        _lib.lib().flour_hip_set_prefill_persistent(persistent)
+        try:
+            ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                               c.block_tables, c.max_seqlen_q, c.scale, out_dtype=torch.float32,
+                               out=out)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_persistent(1)
+        return out
+
+    a, b = go(1), go(0)
+    assert torch.equal(a, b)
+    cu = to_np(c.cu_seqlens_q)
+    assert bool((a[int(cu[7]):int(cu[8])] == 7.0).all())
+    ref, rows = oracle_prefill(c, seqs=[0, 20, 36])
+    max_abs, rel = errors(to_np(a)[rows], ref)
+    print(f"persistent H={H} G={G} max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
