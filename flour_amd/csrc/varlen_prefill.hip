@@ -55,6 +55,9 @@ static constexpr int PF_THREADS = PF_WAVES * 64;
 static constexpr float PF_RESCALE_SLACK = 8.0f;  // log2 units the reference max may lag
 static constexpr int PF_KPITCH = PF_D + 8;   // elements: 272 B rows
 static constexpr int PF_VPITCH = PF_KT + 8;  // elements: 144 B rows
+static constexpr int PF_OPITCH = 68;         // elements: 136 B rows of output staging
+static_assert(4 * 32 * PF_OPITCH <= PF_KT * PF_KPITCH && 4 * 32 * PF_OPITCH <= PF_D * PF_VPITCH,
+              "output staging fits one K / V buffer per head");
 static constexpr float PF_LOG2E = 1.4426950408889634f;
 // Persistent schedule limits (the per-workgroup item table lives in LDS); larger batches use
 // one workgroup per item.
@@ -479,24 +482,51 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 
     // ---- epilogue: lane (h2, q) holds dims 32 mt2 + 8 i + 4 h2 + j of query row wr0 + q
     lsum += wave_shfl_xor(lsum, 32);
-    const int orow = wr0 + ql32;
-    if (wave_active && orow < ql) {
+    if (wave_active) {
         const float inv = 1.0f / lsum;
-        TO* op = out + (int64_t)(q0 + orow) * o_st + (int64_t)head * o_sh + 4 * h2;
+        if constexpr (sizeof(TO) == 4) {
+            const int orow = wr0 + ql32;
+            if (orow < ql) {
+                TO* op = out + (int64_t)(q0 + orow) * o_st + (int64_t)head * o_sh + 4 * h2;
 #pragma unroll
-        for (int mt2 = 0; mt2 < 4; mt2++)
+                for (int mt2 = 0; mt2 < 4; mt2++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                TO* dst = op + 32 * mt2 + 8 * i;
-                const float a0 = o[mt2][4 * i] * inv, a1 = o[mt2][4 * i + 1] * inv;
-                const float a2 = o[mt2][4 * i + 2] * inv, a3 = o[mt2][4 * i + 3] * inv;
-                if constexpr (sizeof(TO) == 4) {
-                    *reinterpret_cast<f32x4*>(dst) = f32x4{a0, a1, a2, a3};
-                } else {
-                    *reinterpret_cast<u32x2*>(dst) =
-                        u32x2{pack2<TO>(a0, a1), pack2<TO>(a2, a3)};
+                    for (int i = 0; i < 4; i++)
+                        *reinterpret_cast<f32x4*>(op + 32 * mt2 + 8 * i) =
+                            f32x4{o[mt2][4 * i] * inv, o[mt2][4 * i + 1] * inv,
+                                  o[mt2][4 * i + 2] * inv, o[mt2][4 * i + 3] * inv};
+            }
+        } else {
+            // 16-bit output goes through LDS (the second K / V buffer, idle until the next
+            // item's first tile is staged, which follows a barrier) in two 64-dim halves, so
+            // that each store writes whole 128 B row segments: lane (r, c) = (lane / 8,
+            // lane % 8) stores dims 8c .. 8c + 7 of rows r, r + 8, r + 16, r + 24.
+            uint16_t* stg = (w < 4 ? &Ks[1][0] : &Vt[1][0]) + (w & 3) * (32 * PF_OPITCH);
+            const int rr = lane >> 3, cc = lane & 7;
+            TO* ob = out + (int64_t)(q0 + wr0) * o_st + (int64_t)head * o_sh + 8 * cc;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const f32x16& x = o[2 * half + mt];
+                        *reinterpret_cast<u32x2*>(&stg[ql32 * PF_OPITCH + 32 * mt + 8 * i + 4 * h2]) =
+                            u32x2{pack2<TO>(x[4 * i] * inv, x[4 * i + 1] * inv),
+                                  pack2<TO>(x[4 * i + 2] * inv, x[4 * i + 3] * inv)};
+                    }
+#pragma unroll
+                for (int s4 = 0; s4 < 4; s4++) {
+                    const int r = rr + 8 * s4;
+                    const uint16_t* src = &stg[r * PF_OPITCH + 8 * cc];
+                    const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+                    const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 4);
+                    if (wr0 + r < ql)
+                        *reinterpret_cast<u32x4*>(ob + (int64_t)r * o_st + 64 * half) =
+                            u32x4{lo[0], lo[1], hi[0], hi[1]};
                 }
             }
+        }
     }
     }  // items
 }
