@@ -63,6 +63,7 @@ static constexpr float PF_LOG2E = 1.4426950408889634f;
 // one workgroup per item.
 static constexpr int PF_MAX_SEQS = 2048;
 static constexpr int PF_MAX_LEVELS = 512;  // query tiles per sequence (65536 rows)
+static constexpr int PF_MAX_WG_ITEMS = 256;  // items per workgroup
 
 __device__ __forceinline__ int swap_bits01(int x) {
     return (x & ~3) | ((x & 1) << 1) | ((x >> 1) & 1);
@@ -112,14 +113,19 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     const int lane = tid & 63;
     const int h2 = lane >> 5, ql32 = lane & 31;
     const int NQ = n_qt_max;
+    const int G = gridDim.x;
+    const int wg = blockIdx.x;
+    const int kv_cap = max_blocks * block_size;  // kv lengths are clamped to the block table
 
     __shared__ int sched_order[PF_MAX_SEQS];       // sequences by decreasing tile count
     __shared__ int sched_more[PF_MAX_LEVELS + 1];  // [v]: sequences with more than v tiles
     __shared__ int sched_fill[PF_MAX_LEVELS + 1];
     __shared__ int sched_cum[PF_MAX_LEVELS + 2];   // [L]: items before level L
+    __shared__ int sched_cu[PF_MAX_SEQS + 1];      // cu_seqlens
+    __shared__ int sched_kv[PF_MAX_SEQS];          // clamped kv lengths
     auto seq_tiles = [&](int sq) {  // query tiles of a sequence (0 if it cannot be served)
-        const int l = cu_seqlens[sq + 1] - cu_seqlens[sq];
-        const int kl = min(kv_lens[sq], max_blocks * block_size);
+        const int l = sched_cu[sq + 1] - sched_cu[sq];
+        const int kl = sched_kv[sq];
         return (l <= 0 || kl < l) ? 0 : min((l + PF_QT - 1) / PF_QT, NQ);
     };
     // exclusive suffix / prefix scans over up to PF_MAX_LEVELS + 1 entries by wave 0
@@ -149,6 +155,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
     int total_items = 0;
     if (persistent) {
+        for (int i = tid; i <= num_seqs; i += PF_THREADS) sched_cu[i] = cu_seqlens[i];
+        for (int i = tid; i < num_seqs; i += PF_THREADS) sched_kv[i] = min(kv_lens[i], kv_cap);
         for (int v = tid; v <= NQ; v += PF_THREADS) sched_fill[v] = 0;
         __syncthreads();
         for (int sq = tid; sq < num_seqs; sq += PF_THREADS) atomicAdd(&sched_fill[seq_tiles(sq)], 1);
@@ -189,76 +197,98 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             if (lane == 0) sched_cum[NQ] = t;
         }
         __syncthreads();
-        total_items = sched_cum[NQ];
+        total_items = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
     }
-    const int G = gridDim.x;
-    int level_hint = 0;
-    for (int round = 0;; round++) {
-        int level, seq, hp;
-        if (persistent) {
-            const int item = round * G + ((round & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x);
-            if (item >= total_items) break;
-            while (sched_cum[level_hint + 1] <= item) level_hint++;  // items only grow
-            level = level_hint;
-            const int j = item - sched_cum[level];
-            seq = sched_order[j / npairs];
-            hp = j - (j / npairs) * npairs;
-        } else {
-            if (round > 0) break;
-            const int per_rank = num_seqs * npairs;
-            const int bid = blockIdx.x;
-            level = bid / per_rank;
-            const int r = bid - level * per_rank;
-            seq = r / npairs;
-            hp = r - seq * npairs;
-        }
-        level = __builtin_amdgcn_readfirstlane(level);
-        seq = __builtin_amdgcn_readfirstlane(seq);
-        hp = __builtin_amdgcn_readfirstlane(hp);
-    const int kvh = hp / pairs_per_kv;
-    const int hj = hp - kvh * pairs_per_kv;
 
-    const int q0 = cu_seqlens[seq];
-    const int ql = cu_seqlens[seq + 1] - q0;
-    // kv lengths are clamped to what the block table can address (a bad length never reads
-    // past the table).
-    const int kv_len = min(kv_lens[seq], max_blocks * block_size);
-    const int qt = n_qt_max - 1 - level;
-    if (qt * PF_QT >= ql || kv_len < ql) continue;
-    const int off = kv_len - ql;
-    const int row_begin = qt * PF_QT;
-    const int row_last = min(row_begin + PF_QT, ql) - 1;
-    const int kv_end = off + row_last + 1;  // exclusive bound of visible kv for this tile
-    const int n_kt = (kv_end + PF_KT - 1) / PF_KT;
+    // ---- this workgroup's items, decoded once into LDS (one thread per item): the k-th item
+    // is number k*G + b on even k and k*G + G-1-b on odd k of the longest-first list
+    // (persistent), or item b alone (one workgroup per item). An entry holds
+    // {seq, qt, kv head, pair in group, q0, q_len, kv_len, kv tiles}.
+    __shared__ __attribute__((aligned(16))) int sched_items[PF_MAX_WG_ITEMS][8];
+    __shared__ int sched_nitems;
+    {
+        int n_items = 0;
+        if (persistent) {
+            const int rounds = total_items / G, rem = total_items - rounds * G;
+            n_items = rounds + (((rounds & 1) ? G - 1 - wg : wg) < rem ? 1 : 0);
+            n_items = min(n_items, PF_MAX_WG_ITEMS);
+        } else {
+            n_items = 1;
+        }
+        for (int k = tid; k < n_items; k += PF_THREADS) {
+            int seq, level, hp, q0, ql, kvl;
+            if (persistent) {
+                const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
+                int lo = 0, hi = NQ - 1;  // last level L with sched_cum[L] <= idx
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (sched_cum[mid] <= idx) lo = mid; else hi = mid - 1;
+                }
+                level = lo;
+                const int j = idx - sched_cum[level];
+                const int r = j / npairs;
+                seq = sched_order[r];
+                hp = j - r * npairs;
+                q0 = sched_cu[seq];
+                ql = sched_cu[seq + 1] - q0;
+                kvl = sched_kv[seq];
+            } else {
+                const int per_rank = num_seqs * npairs;
+                level = wg / per_rank;
+                const int r = wg - level * per_rank;
+                seq = r / npairs;
+                hp = r - seq * npairs;
+                q0 = cu_seqlens[seq];
+                ql = cu_seqlens[seq + 1] - q0;
+                kvl = min(kv_lens[seq], kv_cap);
+            }
+            const int qt = NQ - 1 - level;
+            const int kvh = hp / pairs_per_kv;
+            const int row_last = min(qt * PF_QT + PF_QT, ql) - 1;
+            const bool ok = qt * PF_QT < ql && kvl >= ql;  // always true for persistent items
+            int* e = sched_items[k];
+            e[0] = seq;
+            e[1] = qt;
+            e[2] = kvh;
+            e[3] = hp - kvh * pairs_per_kv;
+            e[4] = q0;
+            e[5] = ql;
+            e[6] = kvl;
+            e[7] = ok ? (kvl - ql + row_last + 1 + PF_KT - 1) / PF_KT : 0;  // causal kv tiles
+            if (!persistent) sched_nitems = ok ? 1 : 0;
+        }
+        if (persistent && tid == 0) sched_nitems = n_items;
+        __syncthreads();
+    }
+    const int n_items = __builtin_amdgcn_readfirstlane(sched_nitems);
+
+    // A work item (all fields workgroup-uniform); valid == 0 past the end of the list.
+    struct Item {
+        int valid, seq, qt, kvh, hj, q0, ql, kv_len, n_kt, last_page;
+    };
+    auto uni = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
+    auto fetch = [&](int k) __attribute__((always_inline)) {
+        Item it{};
+        if (k < n_items) {
+            const int4 a = *reinterpret_cast<const int4*>(&sched_items[k][0]);
+            const int4 b = *reinterpret_cast<const int4*>(&sched_items[k][4]);
+            it.valid = 1;
+            it.seq = uni(a.x);
+            it.qt = uni(a.y);
+            it.kvh = uni(a.z);
+            it.hj = uni(a.w);
+            it.q0 = uni(b.x);
+            it.ql = uni(b.y);
+            it.kv_len = uni(b.z);
+            it.n_kt = uni(b.w);
+            it.last_page = BS16 ? (it.kv_len - 1) >> 4 : (it.kv_len - 1) / block_size;
+        }
+        return it;
+    };
 
     const int hsel = w >> 2;  // which head of the pair
-    const int head = kvh * n_rep + 2 * hj + hsel;
-    const bool head_ok = 2 * hj + hsel < n_rep;
-    const int32_t* bt = block_tables + (int64_t)seq * max_blocks;
     const int max_phys = (int)(num_slots / block_size - 1);
-    const int last_page = (kv_len - 1) / block_size;
     const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(k_pool + (int64_t)kvh * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
-    const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(v_pool + (int64_t)kvh * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
-
-    // ---- this lane's query row and its causal limit (padded rows copy the last valid row)
-    const int wr0 = row_begin + 32 * (w & 3);
-    const bool wave_active = head_ok && wr0 < ql;
-    const int qrow = min(wr0 + ql32, ql - 1);
-    const int lim = off + qrow;                        // visible kv j <= lim
-    const int wave_lim = off + min(wr0 + 31, ql - 1);  // largest limit in the wave
-    const int wave_min_lim = off + wr0;                // smallest limit in the wave
-
-    // Q^T as the B operand: lane (h2, q) holds row q, dims 16kk + 8h2 .. +7.
-    u32x4 qb[8];
-    {
-        const int hq = head_ok ? head : head - 1;  // idle waves read a valid row
-        const T* qp = q + (int64_t)(q0 + qrow) * q_st + (int64_t)hq * q_sh + 8 * h2;
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++) qb[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
-    }
 
     // ---- staging assignment (a 64-token tile is four 16-token groups, each inside one page)
     // K: two 16 B chunks per thread: token (tid / 16) + 32i of the tile, dims (tid % 16) * 8;
@@ -272,15 +302,55 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     const uint32_t k_lane = (uint32_t)((k_row & 15) * D + k_col) * (uint32_t)sizeof(T);
     const uint32_t v_lane = (uint32_t)((2 * v_tp & 15) * D + 8 * v_dg) * (uint32_t)sizeof(T);
     const bool v_g1 = (v_tp >> 3) & 1, v_g2 = (v_tp >> 4) & 1;
-    // Byte offset (in the kv head's pool) of the first token of each group of a tile:
-    // workgroup-uniform, read through the scalar cache. A bad block id is clamped into the
-    // pool; groups past kv_len reuse the last page (their loads are masked off).
+
+    // ---- load context: the item whose K / V tiles are being fetched
+    __amdgpu_buffer_rsrc_t k_rsrc, v_rsrc;
+    const int32_t* bt = block_tables;
+    int kv_len = 0, last_page = 0, n_kt = 0;
+    auto set_load = [&](const Item& it) {
+        k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(k_pool + (int64_t)it.kvh * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
+        v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(v_pool + (int64_t)it.kvh * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
+        bt = block_tables + (int64_t)it.seq * max_blocks;
+        kv_len = it.kv_len;
+        last_page = it.last_page;
+        n_kt = it.n_kt;
+    };
+    // Block ids reach the tile loads through a window of the block table held in VGPRs (lane
+    // i: entry wbase + i in win_cur, wbase + 64 + i in win_next), refilled 64 entries ahead
+    // with vector loads. Scalar loads would share the LDS wait counter, so every LDS wait of a
+    // tile would also wait for them.
+    uint32_t win_cur = 0, win_next = 0, win_pre = 0;  // win_pre: first window of the next item
+    int wbase = 0;
+    auto load_window = [&](const int32_t* row, int base, int n_entries) __attribute__((always_inline)) {
+        const int e = min(base + lane, n_entries - 1);  // entries past the last page are unused
+        return (uint32_t)row[e];
+    };
+    // Byte offset (in the kv head's pool) of the first token of each group of tile kt
+    // (workgroup-uniform). A bad block id is clamped into the pool; groups past kv_len reuse
+    // the last page (their loads are masked off). Tiles are visited in non-decreasing order.
     auto page_bases = [&](int kt, int* pb) {
+        const int lb0 = min(BS16 ? (kt * PF_KT) >> 4 : kt * PF_KT / block_size, last_page);
+        while (lb0 - wbase >= 64) {
+            asm volatile("" ::: "memory");
+            win_cur = win_next;
+            wbase += 64;
+            win_next = load_window(bt, wbase + 64, last_page + 1);
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int tok0 = kt * PF_KT + 16 * i;
             const int lb = min(BS16 ? (tok0 >> 4) : tok0 / block_size, last_page);
-            const int phys = min(max(bt[lb], 0), max_phys);
+            const int idx = lb - wbase;  // < 64 for 16-token pages (a tile's 4 ids are aligned)
+            int id;
+            if (BS16 || idx < 64) {
+                id = __builtin_amdgcn_readlane((int)win_cur, min(idx, 63));
+            } else {
+                asm volatile("" ::: "memory");
+                id = __builtin_amdgcn_readlane((int)win_next, idx - 64);
+            }
+            const int phys = min(max(id, 0), max_phys);
             pb[i] = (int)((uint32_t)(phys * block_size + (tok0 - lb * block_size)) * ROW_BYTES);
         }
     };
@@ -322,14 +392,94 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         }
     };
 
+    // ---- per-item compute state (the item whose tile the workgroup is computing)
+    int head = 0, q0 = 0, ql = 0, wr0 = 0, lim = 0, wave_lim = 0, wave_min_lim = 0;
+    bool wave_active = false;
+    auto set_compute = [&](const Item& it) {
+        head = it.kvh * n_rep + 2 * it.hj + hsel;
+        q0 = it.q0;
+        ql = it.ql;
+        const int off = it.kv_len - it.ql;
+        wr0 = it.qt * PF_QT + 32 * (w & 3);
+        wave_active = (2 * it.hj + hsel < n_rep) && wr0 < it.ql;
+        lim = off + min(wr0 + ql32, it.ql - 1);        // this lane's row sees kv j <= lim
+        wave_lim = off + min(wr0 + 31, it.ql - 1);     // largest limit in the wave
+        wave_min_lim = off + wr0;                      // smallest limit in the wave
+    };
+    // Q^T as the B operand: lane (h2, q) holds row q, dims 16kk + 8h2 .. +7 (idle waves and
+    // padded rows read a valid row)
+    u32x4 qb[8];
+    auto load_q = [&](const Item& it) __attribute__((always_inline)) {
+        const int hd = it.kvh * n_rep + 2 * it.hj + hsel;
+        const int hq = 2 * it.hj + hsel < n_rep ? hd : hd - 1;
+        const int row = min(it.qt * PF_QT + 32 * (w & 3) + ql32, it.ql - 1);
+        const T* qp = q + (int64_t)(it.q0 + row) * q_st + (int64_t)hq * q_sh + 8 * h2;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) qb[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
+    };
+
     // Running state: the reference max m may lag the true running max by up to
     // PF_RESCALE_SLACK (weights then reach 2^8), which skips most accumulator rescales.
     float m = -INFINITY, lsum = 0.0f;
     f32x16 o[4];
+    auto reset_state = [&]() {
+        m = -INFINITY;
+        lsum = 0.0f;
 #pragma unroll
-    for (int x = 0; x < 4; x++)
+        for (int x = 0; x < 4; x++)
 #pragma unroll
-        for (int y = 0; y < 16; y++) o[x][y] = 0.0f;
+            for (int y = 0; y < 16; y++) o[x][y] = 0.0f;
+    };
+    // ---- epilogue: lane (h2, q) holds dims 32 mt2 + 8 i + 4 h2 + j of query row wr0 + q
+    auto store_output = [&]() __attribute__((always_inline)) {
+        const float l = lsum + wave_shfl_xor(lsum, 32);
+        if (wave_active) {
+            const float inv = 1.0f / l;
+            if constexpr (sizeof(TO) == 4) {
+                const int orow = wr0 + ql32;
+                if (orow < ql) {
+                    TO* op = out + (int64_t)(q0 + orow) * o_st + (int64_t)head * o_sh + 4 * h2;
+#pragma unroll
+                    for (int mt2 = 0; mt2 < 4; mt2++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            *reinterpret_cast<f32x4*>(op + 32 * mt2 + 8 * i) =
+                                f32x4{o[mt2][4 * i] * inv, o[mt2][4 * i + 1] * inv,
+                                      o[mt2][4 * i + 2] * inv, o[mt2][4 * i + 3] * inv};
+                }
+            } else {
+                // 16-bit output goes through LDS (the second K / V buffer, idle until the next
+                // item's first tile is staged, which follows a barrier) in two 64-dim halves, so
+                // that each store writes whole 128 B row segments: lane (r, c) = (lane / 8,
+                // lane % 8) stores dims 8c .. 8c + 7 of rows r, r + 8, r + 16, r + 24.
+                uint16_t* stg = (w < 4 ? &Ks[1][0] : &Vt[1][0]) + (w & 3) * (32 * PF_OPITCH);
+                const int rr = lane >> 3, cc = lane & 7;
+                TO* ob = out + (int64_t)(q0 + wr0) * o_st + (int64_t)head * o_sh + 8 * cc;
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const f32x16& x = o[2 * half + mt];
+                            *reinterpret_cast<u32x2*>(&stg[ql32 * PF_OPITCH + 32 * mt + 8 * i + 4 * h2]) =
+                                u32x2{pack2<TO>(x[4 * i] * inv, x[4 * i + 1] * inv),
+                                      pack2<TO>(x[4 * i + 2] * inv, x[4 * i + 3] * inv)};
+                        }
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; s4++) {
+                        const int r = rr + 8 * s4;
+                        const uint16_t* src = &stg[r * PF_OPITCH + 8 * cc];
+                        const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+                        const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 4);
+                        if (wr0 + r < ql)
+                            *reinterpret_cast<u32x4*>(ob + (int64_t)r * o_st + 64 * half) =
+                                u32x4{lo[0], lo[1], hi[0], hi[1]};
+                    }
+                }
+            }
+        }
+    };
 
     // S^T of the tile in flight (64 tokens x 32 queries, two 32-token halves, raw q.k).
     f32x16 st[2];
@@ -442,93 +592,68 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         lsum += psum;
     };
 
-    // ---- pipeline: one barrier per tile; global loads run two tiles ahead of the compute
-    // (register sets A / B alternate), LDS double-buffered, page ids three tiles ahead.
+    // ---- items: while the epilogue of one item stores its output, the Q rows and the first
+    // two K / V tiles of the next one are already in flight. Within an item, one barrier per
+    // tile: global loads run two tiles ahead of the compute (register sets A / B alternate),
+    // LDS double-buffered, page ids three tiles ahead.
+    if (n_items == 0) return;
     u32x4 ka[2], va[2], kb[2], vb[2];
     int pb0[4], pb1[4], pb2[4];
-    page_bases(0, pb0);
-    gload(0, pb0, true, ka, va);
-    page_bases(min(1, n_kt - 1), pb1);
-    gload(1, pb1, 1 < n_kt, kb, vb);
-    page_bases(min(2, n_kt - 1), pb2);
-    // Q must have landed before the loop (its loads precede the tile loads, so this waits for
-    // them alone); otherwise the compiler sinks the Q loads past the first barrier and keeps a
-    // conservative wait for them inside the loop
-#pragma unroll
-    for (int kk = 0; kk < 8; kk++) asm volatile("" ::"v"(qb[kk]));
-    lds_store(0, ka, va);
-    __syncthreads();
-    // step kt: refill `nx` with tile kt + 2, compute tile kt, store tile kt + 1 (held in `st1`)
-    auto step = [&](int kt, u32x4* knx, u32x4* vnx, u32x4* kst1, u32x4* vst1) {
-        gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
-        page_bases(min(kt + 3, n_kt - 1), pb0);
-        if (visible(kt)) {
-            qk(kt & 1);
-            sm_pv(kt, kt & 1);
-        }
-        lds_store((kt + 1) & 1, kst1, vst1);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {  // pb2 <- tile kt + 3
-            const int x = pb2[i];
-            pb2[i] = pb0[i];
-            pb0[i] = x;
-        }
-        __syncthreads();
+    auto prologue = [&](const Item& it, const Item& after) __attribute__((always_inline)) {
+        set_load(it);
+        load_q(it);
+        win_cur = win_pre;
+        wbase = 0;
+        win_next = load_window(bt, 64, last_page + 1);
+        if (after.valid)  // first window of the item after this one
+            win_pre = load_window(block_tables + (int64_t)after.seq * max_blocks, 0,
+                                  after.last_page + 1);
+        page_bases(0, pb0);
+        gload(0, pb0, true, ka, va);
+        page_bases(min(1, n_kt - 1), pb1);
+        gload(1, pb1, 1 < n_kt, kb, vb);
+        page_bases(min(2, n_kt - 1), pb2);
     };
-    for (int kt = 0; kt < n_kt; kt += 2) {
-        step(kt, ka, va, kb, vb);
-        if (kt + 1 < n_kt) step(kt + 1, kb, vb, ka, va);
-    }
-
-    // ---- epilogue: lane (h2, q) holds dims 32 mt2 + 8 i + 4 h2 + j of query row wr0 + q
-    lsum += wave_shfl_xor(lsum, 32);
-    if (wave_active) {
-        const float inv = 1.0f / lsum;
-        if constexpr (sizeof(TO) == 4) {
-            const int orow = wr0 + ql32;
-            if (orow < ql) {
-                TO* op = out + (int64_t)(q0 + orow) * o_st + (int64_t)head * o_sh + 4 * h2;
+    Item ci = fetch(0);
+    win_pre = load_window(block_tables + (int64_t)ci.seq * max_blocks, 0, ci.last_page + 1);
+    prologue(ci, fetch(1));
+    set_compute(ci);
+    for (int k = 0;;) {
+        reset_state();
+        // Q must have landed before the loop (its loads precede the tile loads, so this waits
+        // for them alone); otherwise the compiler sinks the Q loads past the first barrier and
+        // keeps a conservative wait for them inside the loop
 #pragma unroll
-                for (int mt2 = 0; mt2 < 4; mt2++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        *reinterpret_cast<f32x4*>(op + 32 * mt2 + 8 * i) =
-                            f32x4{o[mt2][4 * i] * inv, o[mt2][4 * i + 1] * inv,
-                                  o[mt2][4 * i + 2] * inv, o[mt2][4 * i + 3] * inv};
+        for (int kk = 0; kk < 8; kk++) asm volatile("" ::"v"(qb[kk]));
+        lds_store(0, ka, va);
+        __syncthreads();
+        // step kt: refill `nx` with tile kt + 2, compute tile kt, store tile kt + 1 (in `st1`)
+        auto step = [&](int kt, u32x4* knx, u32x4* vnx, u32x4* kst1, u32x4* vst1) {
+            gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
+            page_bases(min(kt + 3, n_kt - 1), pb0);
+            if (visible(kt)) {
+                qk(kt & 1);
+                sm_pv(kt, kt & 1);
             }
-        } else {
-            // 16-bit output goes through LDS (the second K / V buffer, idle until the next
-            // item's first tile is staged, which follows a barrier) in two 64-dim halves, so
-            // that each store writes whole 128 B row segments: lane (r, c) = (lane / 8,
-            // lane % 8) stores dims 8c .. 8c + 7 of rows r, r + 8, r + 16, r + 24.
-            uint16_t* stg = (w < 4 ? &Ks[1][0] : &Vt[1][0]) + (w & 3) * (32 * PF_OPITCH);
-            const int rr = lane >> 3, cc = lane & 7;
-            TO* ob = out + (int64_t)(q0 + wr0) * o_st + (int64_t)head * o_sh + 8 * cc;
+            lds_store((kt + 1) & 1, kst1, vst1);
 #pragma unroll
-            for (int half = 0; half < 2; half++) {
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const f32x16& x = o[2 * half + mt];
-                        *reinterpret_cast<u32x2*>(&stg[ql32 * PF_OPITCH + 32 * mt + 8 * i + 4 * h2]) =
-                            u32x2{pack2<TO>(x[4 * i] * inv, x[4 * i + 1] * inv),
-                                  pack2<TO>(x[4 * i + 2] * inv, x[4 * i + 3] * inv)};
-                    }
-#pragma unroll
-                for (int s4 = 0; s4 < 4; s4++) {
-                    const int r = rr + 8 * s4;
-                    const uint16_t* src = &stg[r * PF_OPITCH + 8 * cc];
-                    const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
-                    const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 4);
-                    if (wr0 + r < ql)
-                        *reinterpret_cast<u32x4*>(ob + (int64_t)r * o_st + 64 * half) =
-                            u32x4{lo[0], lo[1], hi[0], hi[1]};
-                }
+            for (int i = 0; i < 4; i++) {  // pb2 <- tile kt + 3
+                const int x = pb2[i];
+                pb2[i] = pb0[i];
+                pb0[i] = x;
             }
+            __syncthreads();
+        };
+        for (int kt = 0; kt < n_kt; kt += 2) {
+            step(kt, ka, va, kb, vb);
+            if (kt + 1 < n_kt) step(kt + 1, kb, vb, ka, va);
         }
+        const Item nx = fetch(++k);
+        if (nx.valid) prologue(nx, fetch(k + 1));
+        store_output();
+        if (!nx.valid) break;
+        set_compute(nx);
     }
-    }  // items
 }
 
 static int g_prefill_persistent = 1;  // a tuning / test switch
@@ -556,9 +681,10 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
                                hipStream_t stream) {
     const int64_t n_qt = (max_seqlen_q + PF_QT - 1) / PF_QT;
     const int64_t items = n_qt * num_seqs * (num_heads / n_rep) * ((n_rep + 1) / 2);
+    const int64_t cus = device_cus();
     const bool persistent = g_prefill_persistent && num_seqs <= PF_MAX_SEQS &&
-                            n_qt <= PF_MAX_LEVELS;
-    const int64_t grid = persistent ? std::min<int64_t>(items, device_cus()) : items;
+                            n_qt <= PF_MAX_LEVELS && (items + cus - 1) / cus <= PF_MAX_WG_ITEMS;
+    const int64_t grid = persistent ? std::min<int64_t>(items, cus) : items;
     if (grid > 0x7fffffff) {
         set_error("varlen_prefill: grid too large");
         return FLOUR_ERR_UNSUPPORTED;
