@@ -30,6 +30,9 @@ SIGNATURES: dict[str, tuple] = {
     "flour_hip_version": (ctypes.c_char_p, []),
     "flour_hip_kv_write": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _c_int,
                                     _c_int, _c_i64, _c_int, _vp]),
+    "flour_hip_rope_kv_write": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64,
+                                         _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int,
+                                         _c_int, _c_int, _c_i64, _c_int, _vp]),
     "flour_hip_paged_decode_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int,
                                                        ctypes.POINTER(ctypes.c_size_t)]),
     "flour_hip_paged_decode": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _c_int,

@@ -75,6 +75,61 @@ def kv_write(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_pool: tor
                                    dtype_code(k.dtype), _stream()))
 
 
+def rope_tables(max_pos: int, head_dim: int, rope_theta: float, dtype: torch.dtype,
+                device: torch.device | str = "cpu") -> tuple[torch.Tensor, torch.Tensor]:
+    """The cos / sin tables of Cache::new (src/models/common/cache.rs:377-393), each
+    (max_pos, head_dim / 2): theta_i = 1 / rope_theta^(2i / head_dim) and angle = pos * theta_i
+    in fp32, cos / sin in fp32, then cast to ``dtype``. Computed with torch's fp32 CPU math
+    (the reference uses Rust's f32 powf / cos / sin, which may differ in the last fp32 bit)."""
+    half = head_dim // 2
+    i = torch.arange(half, dtype=torch.float32)
+    theta = 1.0 / torch.pow(torch.tensor(rope_theta, dtype=torch.float32), (2 * i) / head_dim)
+    pos = torch.arange(max_pos, dtype=torch.float32).reshape(max_pos, 1)
+    ang = pos * theta.reshape(1, half)
+    return (ang.cos().to(dtype).contiguous().to(device),
+            ang.sin().to(dtype).contiguous().to(device))
+
+
+def rope_kv_write(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor,
+                  v_pool: torch.Tensor, slot_mapping: torch.Tensor, positions: torch.Tensor,
+                  cos: torch.Tensor, sin: torch.Tensor, q_out: torch.Tensor | None = None
+                  ) -> torch.Tensor:
+    """RoPE on q and k (rotate-half form, each product and sum in the tensor dtype), then
+    k_pool[h, slot_mapping[t], :] = rope(k[t, h, :]) and v_pool[h, slot_mapping[t], :] =
+    v[t, h, :]; returns rope(q) in ``q_out`` (default: a new tensor; ``q_out=q`` rotates in
+    place). ``q`` is (num_tokens, num_heads, head_dim), ``k``/``v`` (num_tokens, kv_heads,
+    head_dim), all with a unit last stride; ``positions`` holds each token's table row."""
+    _need_cuda(q, k, v, k_pool, v_pool, slot_mapping, positions, cos, sin)
+    _need_i32(slot_mapping, positions)
+    T, H, D = q.shape
+    if k.dim() != 3 or k.shape[0] != T or k.shape[2] != D or v.shape != k.shape or \
+            v.stride() != k.stride() or k.stride(2) != 1 or q.stride(2) != 1:
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT,
+                              "q (T, H, D), k/v (T, G, D) sharing strides, unit last strides")
+    G = k.shape[1]
+    if q_out is None:
+        q_out = torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=q.device)
+    if q_out.shape != q.shape or q_out.stride() != q.stride() or q_out.dtype != q.dtype:
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT, "q_out must match q's shape and strides")
+    if k_pool.shape != v_pool.shape or k_pool.shape[0] != G or k_pool.shape[2] != D or \
+            not k_pool.is_contiguous() or not v_pool.is_contiguous():
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT, "pools must be contiguous (kv_heads, num_slots, head_dim)")
+    dts = {q.dtype, k.dtype, v.dtype, k_pool.dtype, v_pool.dtype, cos.dtype, sin.dtype}
+    if len(dts) != 1:
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT, "q, k, v, pools and tables must share a dtype")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D // 2 or \
+            not cos.is_contiguous() or not sin.is_contiguous():
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT, "tables must be contiguous (max_pos, head_dim / 2)")
+    if slot_mapping.numel() != T or positions.numel() != T:
+        raise _lib.FlourError(_lib.ERR_INVALID_ARGUMENT, "one slot and one position per token")
+    check(lib().flour_hip_rope_kv_write(_ptr(q_out), _ptr(q), q.stride(0), q.stride(1), H,
+                                        _ptr(k), _ptr(v), k.stride(0), k.stride(1),
+                                        _ptr(k_pool), _ptr(v_pool), _ptr(slot_mapping),
+                                        _ptr(positions), _ptr(cos), _ptr(sin), cos.shape[0], T,
+                                        G, D, k_pool.shape[1], dtype_code(q.dtype), _stream()))
+    return q_out
+
+
 def decode_workspace_bytes(batch: int, num_heads: int, kv_heads: int, head_dim: int,
                            max_context_len: int) -> int:
     n = ctypes.c_size_t(0)

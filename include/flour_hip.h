@@ -73,6 +73,33 @@ int flour_hip_kv_write(const void* k, const void* v, int64_t stride_tok, int64_t
                        int kv_heads, int head_dim, int64_t num_slots, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * RoPE + KV-cache write, fused (the step before kernel (1) in the reference, now one pass).
+ * Replaces, at src/models/common/attention.rs:96-104, rope(q) and rope(k)
+ * (candle_nn::rotary_emb::rope: the non-interleaved "rotate half" form) with the cos / sin
+ * tables of Cache::new (cache.rs:377-393) read at the token's position (Cache::rope_cos /
+ * rope_sin narrow them to index_pos.., cache.rs:404-410), then Cache::write_kv
+ * (cache.rs:451-453 -> PagedKvPool::write's scatter, paged.rs:186-187).
+ *
+ * For token t with table row p = positions[t] and i < head_dim / 2, c = cos[p][i],
+ * s = sin[p][i], a row x is rotated to
+ *   y[i] = x[i]·c - x[i + head_dim/2]·s,   y[i + head_dim/2] = x[i]·s + x[i + head_dim/2]·c
+ * with every product and sum rounded to `dtype` (fp32: no contraction). Then
+ *   q_out[t, h, :] = rope(q[t, h, :])                               h < num_heads
+ *   k_pool[h, slot_mapping[t], :] = rope(k[t, h, :]),  v_pool[h, slot_mapping[t], :] = v[t, h, :]
+ * q and q_out share the strides (q_out may be q: in place); k and v share kv_stride_*.
+ * cos_table / sin_table: (max_pos, head_dim / 2) row-major in `dtype`. head_dim must be even.
+ * A token whose slot is outside [0, num_slots) writes no K/V (its q row is still rotated);
+ * one whose position is outside [0, max_pos) writes nothing.
+ * ---------------------------------------------------------------------------------------- */
+int flour_hip_rope_kv_write(void* q_out, const void* q, int64_t q_stride_tok,
+                            int64_t q_stride_head, int num_heads, const void* k, const void* v,
+                            int64_t kv_stride_tok, int64_t kv_stride_head, void* k_pool,
+                            void* v_pool, const int32_t* slot_mapping, const int32_t* positions,
+                            const void* cos_table, const void* sin_table, int max_pos,
+                            int num_tokens, int kv_heads, int head_dim, int64_t num_slots,
+                            int dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Kernel (2): paged decode attention (one new query token per sequence).
  * Replaces paged_attention (src/backend/cpu.rs:57-112) for seq_q == 1, batched over sequences,
  * with the block list of Cache::kv_blocks (cache.rs:456-458 -> KvCache::gather_blocks

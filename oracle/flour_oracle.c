@@ -15,6 +15,8 @@
  *   src/models/common/cache.rs:83-96     KvCache::gather_blocks (logical block list)
  *   src/backend/cpu.rs:57-112            paged_attention (online softmax over blocks)
  *   src/backend/cpu.rs:24-42, :148-165   causal_attention / dense_reference (fp64 here)
+ *   src/models/common/attention.rs:96-104  rope(q), rope(k) (candle_nn::rotary_emb::rope with
+ *                                        the cache.rs:377-393 tables), then write_kv
  *
  * Arithmetic: fp32 as in the reference's accumulation (cpu.rs:71-73, :84-85, :104); bf16/f16
  * inputs are widened exactly to fp32 (the "fp32 CPU reference"), the dense check runs in
@@ -149,6 +151,8 @@ enum {
     MUT_NO_SCALE = 4,         /* drop the softmax scale                           */
     MUT_OFFSET_ZERO = 5,      /* causal offset 0 instead of kv_len - q_len        */
     MUT_SLOT_SWAP = 6,        /* slot = pos%bs * nblk + blk (transposed index)    */
+    MUT_ROPE_INTERLEAVED = 7, /* rotate pairs (2i, 2i+1) instead of (i, i + d/2)  */
+    MUT_ROPE_SIGN = 8,        /* rotate by -angle (sin sign flipped)              */
 };
 static int g_mutation = MUT_NONE;
 void oracle_set_mutation(int code) { g_mutation = code; }
@@ -196,6 +200,83 @@ int64_t oracle_kv_write_scatter(const void* k, const void* v, int64_t stride_tok
         }
     }
     return bad;
+}
+
+/* ---------------------------------------------------------------- attention.rs:96-104 */
+
+/* Round to the element type and back (fp32: unchanged). */
+static inline float round_dt(float x, int dt) {
+    if (dt == DT_F32) return x;
+    if (dt == DT_BF16) return bf16_to_f32(f32_to_bf16_rne(x));
+    return f16_to_f32(f32_to_f16_rne(x));
+}
+
+/* One row of candle_nn::rotary_emb::rope (candle-nn 0.9.2; not vendored here), the
+ * non-interleaved ("rotate half") form that attention.rs:98-99 calls: for i < d/2 with
+ * c = cos[p][i], s = sin[p][i],
+ *   dst[i]       = x[i] * c - x[i + d/2] * s
+ *   dst[i + d/2] = x[i] * s + x[i + d/2] * c
+ * evaluated in the element type: half::bf16 / half::f16 operations compute in f32 and round the
+ * result to the type (nearest even), f32 rounds each operation (no fused multiply-add: this
+ * function is compiled without contraction). The reference's own tests hold no RoPE vectors;
+ * the closed forms in tests/test_oracle.py pin the rotation (identity at position 0, exact
+ * quarter turns, fp64 rotation within the per-step roundings), not the last bit of the
+ * rounding sequence. src may equal dst. */
+__attribute__((optimize("fp-contract=off"))) static void rope_row(
+    void* dst, int64_t dst_off, const void* src, int64_t src_off, const void* cos_t,
+    const void* sin_t, int64_t tab_off, int d, int dt) {
+    const int half = d / 2;
+    for (int i = 0; i < half; i++) {
+        int i1 = i, i2 = i + half;
+        if (g_mutation == MUT_ROPE_INTERLEAVED) {
+            i1 = 2 * i;
+            i2 = 2 * i + 1;
+        }
+        const float x1 = load_elem(src, src_off + i1, dt), x2 = load_elem(src, src_off + i2, dt);
+        const float c = load_elem(cos_t, tab_off + i, dt);
+        float sn = load_elem(sin_t, tab_off + i, dt);
+        if (g_mutation == MUT_ROPE_SIGN) sn = -sn;
+        const float a = round_dt(x1 * c, dt), b = round_dt(x2 * sn, dt);
+        const float e = round_dt(x1 * sn, dt), f = round_dt(x2 * c, dt);
+        store_elem(dst, dst_off + i1, dt, round_dt(a - b, dt));
+        store_elem(dst, dst_off + i2, dt, round_dt(e + f, dt));
+    }
+}
+
+/* RoPE on the new q / k rows, then Cache::write_kv's scatter (paged.rs:186-187): the order of
+ * attention.rs:96-104 for token t at table row positions[t]. q / q_out share strides (in place
+ * allowed); k / v share kv strides; tables are (max_pos, d/2). A token whose slot is outside
+ * [0, num_slots) writes no K/V; one whose position is outside [0, max_pos) writes nothing.
+ * Returns the number of tokens skipped for their position. */
+int64_t oracle_rope_kv_write(void* q_out, const void* q, int64_t q_stride_tok,
+                             int64_t q_stride_head, int num_heads, const void* k, const void* v,
+                             int64_t kv_stride_tok, int64_t kv_stride_head, void* k_pool,
+                             void* v_pool, const int32_t* slots, const int32_t* positions,
+                             const void* cos_t, const void* sin_t, int max_pos, int num_tokens,
+                             int kv_heads, int head_dim, int64_t num_slots, int dtype) {
+    const int es = elem_size(dtype);
+    int64_t skipped = 0;
+    for (int t = 0; t < num_tokens; t++) {
+        const int p = positions[t];
+        if (p < 0 || p >= max_pos) {
+            skipped++;
+            continue;
+        }
+        const int64_t tab = (int64_t)p * (head_dim / 2);
+        for (int h = 0; h < num_heads; h++) {
+            const int64_t off = (int64_t)t * q_stride_tok + (int64_t)h * q_stride_head;
+            rope_row(q_out, off, q, off, cos_t, sin_t, tab, head_dim, dtype);
+        }
+        const int64_t sl = slots[t];
+        if (sl < 0 || sl >= num_slots) continue;
+        for (int h = 0; h < kv_heads; h++) {
+            const int64_t src = (int64_t)t * kv_stride_tok + (int64_t)h * kv_stride_head;
+            const int64_t dst = ((int64_t)h * num_slots + sl) * head_dim;
+            rope_row(k_pool, dst, k, src, cos_t, sin_t, tab, head_dim, dtype);
+            memcpy((char*)v_pool + dst * es, (const char*)v + src * es, (size_t)head_dim * es);
+        }
+    }
+    return skipped;
 }
 
 /* Literal restatement of the run loop at paged.rs:192-202, including the run condition at

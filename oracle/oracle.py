@@ -9,6 +9,8 @@ Functions mirror the reference (lltsdyp/flour) — see flour_oracle.c for file:l
   kv_write_reference_loop       src/models/common/paged.rs:192-202 (literal loop, :196 quirk)
   paged_attention               src/backend/cpu.rs:57-112
   dense_attention_f64           src/backend/cpu.rs:24-42, :148-165 (in fp64)
+  rope_kv_write                 src/models/common/attention.rs:96-104 (rope(q), rope(k) as
+                                candle_nn::rotary_emb::rope, then the write_kv scatter)
 """
 from __future__ import annotations
 
@@ -26,6 +28,7 @@ _NP_CODE = {np.dtype(np.float32): F32}
 
 MUT_NONE, MUT_MASK_OFF_BY_ONE, MUT_NO_CORRECTION, MUT_WRONG_KV_HEAD = 0, 1, 2, 3
 MUT_NO_SCALE, MUT_OFFSET_ZERO, MUT_SLOT_SWAP = 4, 5, 6
+MUT_ROPE_INTERLEAVED, MUT_ROPE_SIGN = 7, 8
 
 _lib = None
 _vp, _i64, _int, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -53,6 +56,10 @@ def lib() -> ctypes.CDLL:
                                                      _int]
         L.oracle_kv_write_quirk_index.restype = _int
         L.oracle_kv_write_quirk_index.argtypes = [_vp, _int]
+        L.oracle_rope_kv_write.argtypes = [_vp, _vp, _i64, _i64, _int, _vp, _vp, _i64, _i64, _vp,
+                                           _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _i64,
+                                           _int]
+        L.oracle_rope_kv_write.restype = _i64
         L.oracle_paged_attention.restype = _int
         L.oracle_paged_attention.argtypes = [_vp, _int, _i64, _i64, _vp, _int, _i64, _i64, _vp, _vp,
                                              _int, _i64, _vp, _int, _vp, _vp, _int, _int, _int, _int,
@@ -152,6 +159,32 @@ def kv_write_reference_loop(k_ref: np.ndarray, v_ref: np.ndarray, k_pool: np.nda
 def kv_write_quirk_index(slots_u32: np.ndarray) -> int:
     s = np.ascontiguousarray(slots_u32, dtype=np.uint32)
     return int(lib().oracle_kv_write_quirk_index(_p(s), s.size))
+
+
+def rope_kv_write(q: np.ndarray, k: np.ndarray, v: np.ndarray, k_pool: np.ndarray,
+                  v_pool: np.ndarray, slot_mapping: np.ndarray, positions: np.ndarray,
+                  cos: np.ndarray, sin: np.ndarray, bf16: bool = True,
+                  q_out: np.ndarray | None = None) -> tuple[np.ndarray, int]:
+    """RoPE on q (T, H, D) and k (T, G, D), then the scatter of rope(k) and v into the pools
+    (in place). Returns (rope(q), tokens skipped for their position); rows of skipped tokens
+    keep what ``q_out`` held (a new uninitialised array by default). Tables (max_pos, D/2)."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    cos = np.ascontiguousarray(cos)
+    sin = np.ascontiguousarray(sin)
+    T, H, D = q.shape
+    G = k.shape[1]
+    assert k_pool.flags.c_contiguous and v_pool.flags.c_contiguous
+    sm = np.ascontiguousarray(slot_mapping, dtype=np.int32)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    if q_out is None:
+        q_out = np.empty_like(q)
+    assert q_out.shape == q.shape and q_out.dtype == q.dtype and q_out.flags.c_contiguous
+    n = lib().oracle_rope_kv_write(_p(q_out), _p(q), H * D, D, H, _p(k), _p(v), G * D, D,
+                                   _p(k_pool), _p(v_pool), _p(sm), _p(pos), _p(cos), _p(sin),
+                                   cos.shape[0], T, G, D, k_pool.shape[1], _code(q, bf16))
+    return q_out, int(n)
 
 
 # ------------------------------------------------------------------ cpu.rs
