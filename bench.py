@@ -147,6 +147,32 @@ def cpu_decode_baseline(case, seconds: float):
     return med, threads, len(times)
 
 
+def cpu_rope_baseline(case, theta: float):
+    """Oracle RoPE + KV write over the whole batch on host copies; (median seconds, runs)."""
+    import numpy as np
+    import torch
+
+    from flour_amd import ops
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O  # noqa: E402
+
+    def host(t):
+        t = t.detach().cpu().contiguous()
+        return t.view(torch.int16).numpy().view(np.uint16) if t.dtype in (torch.bfloat16, torch.float16) else t.numpy()
+
+    pos, cos, sin = rope_inputs(torch, ops, case, theta)
+    args = [host(case.q), host(case.k_new), host(case.v_new), host(case.k_pool).copy(),
+            host(case.v_pool).copy(), host(case.slot_mapping), host(pos), host(cos), host(sin)]
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        O.rope_kv_write(*args, bf16=(case.q.dtype == torch.bfloat16))
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
 def cpu_prefill_baseline(case, seconds: float):
     """Oracle on the shortest sequence of a prefill batch (bounded sample); returns TFLOP/s."""
     import numpy as np
@@ -222,7 +248,30 @@ def bench_decode(torch, ops, case, steps, warmup, graph: bool = False):
                 gbs_step=nbytes / (wall_ms * 1e-3) / 1e9, gbs_kernel=nbytes / (kern_ms * 1e-3) / 1e9)
 
 
-def bench_prefill(torch, ops, case, steps, warmup):
+ROPE_THETA = {"prefill_bf16_varlen_llama3_8b": 500000.0, "prefill_bf16_prefix_qwen2_7b": 1000000.0}
+
+
+def rope_inputs(torch, ops, case, theta):
+    """Each new row's position (kv_len - q_len + i within its sequence) and the cos / sin
+    tables up to the longest sequence."""
+    cu = case.cu_seqlens_q.cpu().tolist()
+    kl = case.kv_lens.cpu().tolist()
+    pos = torch.cat([torch.arange(kl[s] - (cu[s + 1] - cu[s]), kl[s], dtype=torch.int32)
+                     for s in range(len(kl))]).to(case.q.device)
+    cos, sin = ops.rope_tables(max(kl), case.q.shape[2], theta, case.q.dtype, case.q.device)
+    return pos, cos, sin
+
+
+def rope_bytes(case) -> int:
+    """Fused RoPE + KV write: read + write of every q, k and v row, one table row (cos and
+    sin halves) and the slot / position per token."""
+    T, H, D = case.q.shape
+    G = case.k_new.shape[1]
+    es = case.q.element_size()
+    return 2 * T * (H + 2 * G) * D * es + T * D * es + 8 * T
+
+
+def bench_prefill(torch, ops, case, steps, warmup, theta=500000.0):
     out = torch.empty_like(case.q)
 
     def write():
@@ -237,21 +286,31 @@ def bench_prefill(torch, ops, case, steps, warmup):
         write()
         attn()
 
+    pos, cos, sin = rope_inputs(torch, ops, case, theta)
+    q_rot = torch.empty_like(case.q)
+
+    def rope():
+        ops.rope_kv_write(case.q, case.k_new, case.v_new, case.k_pool, case.v_pool,
+                          case.slot_mapping, pos, cos, sin, q_out=q_rot)
+
     wall_ms, _ = event_timed(torch, step, steps, warmup)
     _, per_w = event_timed(torch, write, steps, 1)
     _, per_a = event_timed(torch, attn, steps, 1)
+    _, per_r = event_timed(torch, rope, steps, 1)
     w_ms = sum(per_w) / len(per_w)
     a_ms = sum(per_a) / len(per_a)
+    r_ms = sum(per_r) / len(per_r)
     flops = case.flops()
     return dict(ms_per_step=wall_ms, attn_ms=a_ms, write_ms=w_ms, flops=flops,
                 tflops=flops / (a_ms * 1e-3) / 1e12, write_bytes=case.write_bytes(),
                 write_gbs=case.write_bytes() / (w_ms * 1e-3) / 1e9,
-                causal_pairs=case.causal_pairs())
+                causal_pairs=case.causal_pairs(), rope_ms=r_ms, rope_bytes=rope_bytes(case),
+                rope_gbs=rope_bytes(case) / (r_ms * 1e-3) / 1e9)
 
 
 def prefill_line(torch, ops, case, name, cfg, args):
     """One JSON line for a prefill workload (KV write + causal varlen prefill per step)."""
-    r = bench_prefill(torch, ops, case, args.steps, args.warmup)
+    r = bench_prefill(torch, ops, case, args.steps, args.warmup, ROPE_THETA.get(name, 500000.0))
     line = {
         "metric": "causal varlen prefill attention throughput (useful causal FLOPs)",
         "value": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 2),
@@ -269,8 +328,14 @@ def prefill_line(torch, ops, case, name, cfg, args):
                      "avg_launch_us": round(r["attn_ms"] * 1e3, 3), "traffic": read_traffic(name)},
         "kv_write": {"GB/s": round(r["write_gbs"], 1), "avg_launch_us": round(r["write_ms"] * 1e3, 3),
                      "bytes": r["write_bytes"]},
+        "rope_kv_write": {"GB/s": round(r["rope_gbs"], 1), "hbm_frac": round(r["rope_gbs"] / HBM_PEAK_GBS, 4),
+                          "avg_launch_us": round(r["rope_ms"] * 1e3, 3), "bytes": r["rope_bytes"]},
     }
     if not args.no_cpu:
+        rs, rn = cpu_rope_baseline(case, ROPE_THETA.get(name, 500000.0))
+        line["rope_kv_write"]["cpu_GB/s"] = round(r["rope_bytes"] / rs / 1e9, 3)
+        line["rope_kv_write"]["cpu_sample"] = (f"full batch, median of {rn} runs of the C "
+                                               "restatement (attention.rs:96-104), 1 thread")
         tf, th, reps, S, P = cpu_prefill_baseline(case, args.cpu_seconds)
         line["cpu_baseline"] = {"value": round(tf, 5), "unit": "TFLOP/s", "cores": th, "kind": "port",
                                 "sample": f"shortest sequence of the batch (q_len {S}, prefix {P}), "
@@ -364,12 +429,14 @@ def main():
                              "avg_launch_us": round(rr["kernel_ms"] * 1e3, 2),
                              "algorithmic_bytes": rr["bytes"]}
             else:
-                rr = bench_prefill(torch, ops, cs, args.steps, args.warmup)
+                rr = bench_prefill(torch, ops, cs, args.steps, args.warmup, ROPE_THETA.get(nm, 500000.0))
                 e = {"TFLOP/s": round(rr["tflops"], 1),
                      "mfma_frac": round(rr["tflops"] / BF16_PEAK_TFLOPS, 4),
                      "attn_us": round(rr["attn_ms"] * 1e3, 2), "flops": rr["flops"],
                      "kv_write_GB/s": round(rr["write_gbs"], 1),
                      "kv_write_us": round(rr["write_ms"] * 1e3, 2),
+                     "rope_kv_write_GB/s": round(rr["rope_gbs"], 1),
+                     "rope_kv_write_us": round(rr["rope_ms"] * 1e3, 2),
                      "step_ms": round(rr["ms_per_step"], 4)}
                 if not args.no_cpu:
                     tf, th, reps, S, P = cpu_prefill_baseline(cs, 3.0)
