@@ -78,6 +78,10 @@ SIGNATURES: dict[str, tuple] = {
     "flour_kv_cache_match_prefix": (_c_int, [_vp, _vp, _c_int]),
     "flour_kv_cache_register_prefix": (_c_int, [_vp, _vp, _c_int]),
     "flour_kv_cache_clear_prefix_cache": (_c_int, [_vp]),
+    "flour_kv_cache_export_bundle": (_c_int, [_vp, ctypes.c_char_p, _vp, _c_int, _c_int, _vp, _c_sz,
+                                              ctypes.POINTER(ctypes.c_size_t), _vp]),
+    "flour_kv_cache_import_bundle": (_c_int, [_vp, _vp, _c_sz, _vp, _c_int,
+                                              ctypes.POINTER(ctypes.c_int), _vp]),
     "flour_kv_cache_pool": (_c_int, [_vp, _c_int, _vp, _vp, _vp]),
 }
 

@@ -12,16 +12,24 @@
 // tokens and rejects a lookup whose tokens differ (hash collisions never return wrong KV).
 // The hash function is this file's own (the reference uses Rust's DefaultHasher); only the
 // identity of prefix paths matters, the values are never stored outside the process.
+//
+// Bundles: export_bundle / import_bundle restate Cache::export_prefix_bundle /
+// import_prefix_bundle (cache.rs:166-340) with KvBundleCodec::encode / decode
+// (src/kv_cache/bundle.rs:108-214) on the FLKV frame; the payload moves between the device pools
+// and the host bytes through a device staging buffer (kv_bundle.hip packs / unpacks it).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <unordered_map>
 #include <vector>
 
+#include "flkv_codec.h"
 #include "flour_cache.h"
 #include "flour_common.h"
 #include "flour_hip.h"
+#include "kv_bundle.h"
 
 namespace flour {
 namespace host {
@@ -151,6 +159,9 @@ struct KvCacheImpl {
     bool meta_pending = false;
     void* d_ws = nullptr;
     size_t ws_bytes = 0;
+    void** d_pool_ptrs = nullptr;  // device copy of the K pool addresses, then the V ones
+    void* d_stage = nullptr;       // bundle staging, whole logical blocks (allocated on use)
+    size_t stage_bytes = 0;
     uint64_t table_version = 1, uploaded_version = 0;
     int uploaded_len = -1;
 
@@ -185,6 +196,8 @@ struct KvCacheImpl {
         if (d_meta) (void)hipFree(d_meta);
         if (h_meta) (void)hipHostFree(h_meta);
         if (d_ws) (void)hipFree(d_ws);
+        if (d_pool_ptrs) (void)hipFree(d_pool_ptrs);
+        if (d_stage) (void)hipFree(d_stage);
     }
 
     int alloc_device() {
@@ -209,6 +222,14 @@ struct KvCacheImpl {
                                                   &ws_bytes) != FLOUR_OK)
             return FLOUR_ERR_INVALID_ARGUMENT;
         if (ws_bytes && check_hip(hipMalloc(&d_ws, ws_bytes), "kv_cache: decode workspace"))
+            return FLOUR_ERR_HIP;
+        std::vector<void*> ptrs(k_pools);
+        ptrs.insert(ptrs.end(), v_pools.begin(), v_pools.end());
+        if (check_hip(hipMalloc(&d_pool_ptrs, ptrs.size() * sizeof(void*)),
+                      "kv_cache: pool address table") ||
+            check_hip(hipMemcpy(d_pool_ptrs, ptrs.data(), ptrs.size() * sizeof(void*),
+                                hipMemcpyHostToDevice),
+                      "kv_cache: pool address table"))
             return FLOUR_ERR_HIP;
         device = true;
         return FLOUR_OK;
@@ -328,6 +349,238 @@ struct KvCacheImpl {
 
     void clear_prefix_cache() {
         for (int id : registry.drain_block_ids()) allocator.decref(id);
+    }
+
+    // ---- FLKV bundles
+    size_t bundle_block_bytes() const {  // one logical block of every layer, K and V
+        return (size_t)num_layers * 2 * kv_heads * block_size * head_dim * elem_bytes(dtype);
+    }
+    static constexpr size_t STAGE_CAP = 64u << 20;  // staging chunk, whole logical blocks
+    // Blocks per staging chunk for a bundle of nb logical blocks; grows the buffer on demand.
+    int stage_blocks(int nb) {
+        const size_t per = bundle_block_bytes();
+        const int cb = (int)std::max<size_t>(1, std::min<size_t>(nb, STAGE_CAP / per));
+        const size_t need = (size_t)cb * per;
+        if (need > stage_bytes) {
+            if (d_stage) (void)hipFree(d_stage);
+            d_stage = nullptr;
+            stage_bytes = 0;
+            if (check_hip(hipMalloc(&d_stage, need), "kv bundle: staging allocation")) return -1;
+            stage_bytes = need;
+        }
+        return cb;
+    }
+
+    int export_bundle(const char* model_id, const uint32_t* ids, int n_ids, int token_count,
+                      void* out, size_t cap, size_t* out_len, hipStream_t s) {
+        const int bs = table.block_size();
+        if (token_count <= 0 || token_count % bs != 0) {
+            set_error("export token_count %d not aligned to block size %d", token_count, bs);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (token_count > table.len()) {
+            set_error("export token_count %d exceeds live len %d", token_count, table.len());
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (n_ids < token_count || !ids) {
+            set_error("token_ids len %d shorter than token_count %d", ids ? n_ids : 0, token_count);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        flkv::Meta m;
+        m.model_id = model_id ? model_id : "";
+        m.token_count = (uint64_t)token_count;
+        m.token_ids.assign(ids, ids + token_count);
+        m.block_size = (uint64_t)bs;
+        m.num_layers = (uint64_t)num_layers;
+        m.num_kv_heads = (uint64_t)kv_heads;
+        m.head_dim = (uint64_t)head_dim;
+        m.dtype = dtype;
+        const std::string hdr = flkv::encode_header(m);
+        const int nb = token_count / bs;
+        const size_t per = bundle_block_bytes();
+        const size_t head_end = flkv::PREFIX + hdr.size();
+        const size_t total = head_end + (size_t)nb * per;
+        *out_len = total;
+        if (!out) return FLOUR_OK;  // size query
+        if (cap < total) {
+            set_error("kv bundle: output buffer of %zu bytes, the bundle needs %zu", cap, total);
+            return FLOUR_ERR_CAPACITY;
+        }
+        if (!device) {
+            set_error("kv_cache: no device pool");
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        uint8_t* o = static_cast<uint8_t*>(out);
+        memcpy(o, flkv::MAGIC, 4);
+        o[4] = (uint8_t)(flkv::VERSION & 0xff);
+        o[5] = (uint8_t)(flkv::VERSION >> 8);
+        const uint32_t hl = (uint32_t)hdr.size();
+        for (int i = 0; i < 4; i++) o[6 + i] = (uint8_t)(hl >> (8 * i));
+        memcpy(o + flkv::PREFIX, hdr.data(), hdr.size());
+        int rc = upload_table(1, s);
+        if (rc) return rc;
+        const int cb = stage_blocks(nb);
+        if (cb < 0) return FLOUR_ERR_HIP;
+        for (int b0 = 0; b0 < nb; b0 += cb) {
+            const int n = std::min(cb, nb - b0);
+            rc = launch_kv_bundle_copy(0, d_stage, d_pool_ptrs, d_table(), b0, n, num_layers,
+                                       kv_heads, block_size, head_dim, num_slots,
+                                       elem_bytes(dtype), s);
+            if (rc) return rc;
+            if (check_hip(hipMemcpyAsync(o + head_end + (size_t)b0 * per, d_stage, (size_t)n * per,
+                                         hipMemcpyDeviceToHost, s),
+                          "kv bundle: device-to-host copy"))
+                return FLOUR_ERR_HIP;
+        }
+        return check_hip(hipStreamSynchronize(s), "kv bundle: export");
+    }
+
+    int import_bundle(const void* bytes, size_t len, const uint32_t* prompt, int n_prompt,
+                      int* imported, hipStream_t s) {
+        // ---- KvBundleCodec::decode (bundle.rs:145-214)
+        const uint8_t* p = static_cast<const uint8_t*>(bytes);
+        if (!p || len < flkv::PREFIX) {
+            set_error("bundle too short: %zu bytes", p ? len : (size_t)0);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (memcmp(p, flkv::MAGIC, 4) != 0) {
+            set_error("bad bundle magic");
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        const unsigned version = (unsigned)p[4] | ((unsigned)p[5] << 8);
+        if (version != flkv::VERSION) {
+            set_error("unsupported bundle version %u", version);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        const size_t hl = (size_t)p[6] | ((size_t)p[7] << 8) | ((size_t)p[8] << 16) |
+                          ((size_t)p[9] << 24);
+        const size_t head_end = flkv::PREFIX + hl;
+        if (len < head_end) {
+            set_error("bundle header truncated");
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        flkv::Meta m;
+        flkv::Reader rd(reinterpret_cast<const char*>(p + flkv::PREFIX), hl);
+        if (!rd.parse(m)) {
+            set_error("bundle header: %s", rd.err.c_str());
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (m.block_size == 0) {
+            set_error("bundle block_size is zero");
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (m.token_count == 0 || m.token_count % m.block_size != 0) {
+            set_error("bundle token_count %llu not block aligned to %llu",
+                      (unsigned long long)m.token_count, (unsigned long long)m.block_size);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (m.token_ids.size() != m.token_count) {
+            set_error("bundle token_ids len %zu != token_count %llu", m.token_ids.size(),
+                      (unsigned long long)m.token_count);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        const uint64_t nb64 = m.token_count / m.block_size;
+        // expected payload, with overflow checks (sizes come from the wire)
+        unsigned __int128 expected = (unsigned __int128)nb64 * m.num_layers * 2 * m.num_kv_heads *
+                                     m.block_size * m.head_dim * flkv::dtype_bytes(m.dtype);
+        if (expected != (unsigned __int128)(len - head_end)) {
+            set_error("bundle payload length %zu != expected %llu", len - head_end,
+                      expected >> 64 ? ~0ull : (unsigned long long)expected);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        // ---- Cache::import_prefix_bundle (cache.rs:238-340)
+        const int bs = table.block_size();
+        if (m.block_size != (uint64_t)bs) {
+            set_error("bundle block_size %llu != cache block_size %d",
+                      (unsigned long long)m.block_size, bs);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (m.num_layers != (uint64_t)num_layers) {
+            set_error("bundle num_layers %llu != model %d", (unsigned long long)m.num_layers,
+                      num_layers);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (m.num_kv_heads != (uint64_t)kv_heads) {
+            set_error("bundle num_kv_heads %llu != model %d",
+                      (unsigned long long)m.num_kv_heads, kv_heads);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (m.head_dim != (uint64_t)head_dim) {
+            set_error("bundle head_dim %llu != model %d", (unsigned long long)m.head_dim,
+                      head_dim);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (m.dtype != dtype) {
+            set_error("bundle dtype %s != model dtype", flkv::dtype_name(m.dtype));
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        const uint64_t tc = m.token_count;
+        if (!prompt || n_prompt < 0 || (uint64_t)n_prompt < tc ||
+            memcmp(prompt, m.token_ids.data(), tc * sizeof(uint32_t)) != 0) {
+            set_error("prompt does not start with bundle token ids");
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        if (!device) {
+            set_error("kv_cache: no device pool");
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        const int nb = (int)nb64;
+        // start a clean sequence, then make sure every imported block fits
+        reset_sequence();
+        if (allocator.num_free() < nb) {
+            set_error("not enough free kv blocks to import (%d < %d)", allocator.num_free(), nb);
+            return FLOUR_ERR_OUT_OF_BLOCKS;
+        }
+        std::vector<int> allocated;
+        allocated.reserve(nb);
+        auto roll_back = [&](int rc) {
+            for (int id : allocated) allocator.decref(id);
+            table.clear();
+            table_version++;
+            return rc;
+        };
+        for (int b = 0; b < nb; b++) {
+            const int id = allocator.allocate();
+            if (id < 0) {
+                set_error("out of kv blocks");
+                return roll_back(FLOUR_ERR_OUT_OF_BLOCKS);
+            }
+            allocated.push_back(id);
+            table.push_block(id);
+        }
+        table_version++;
+        int rc = upload_table(1, s);
+        if (rc) return roll_back(rc);
+        const size_t per = bundle_block_bytes();
+        const int cb = stage_blocks(nb);
+        if (cb < 0) return roll_back(FLOUR_ERR_HIP);
+        for (int b0 = 0; b0 < nb; b0 += cb) {
+            const int n = std::min(cb, nb - b0);
+            if (check_hip(hipMemcpyAsync(d_stage, p + head_end + (size_t)b0 * per, (size_t)n * per,
+                                         hipMemcpyHostToDevice, s),
+                          "kv bundle: host-to-device copy"))
+                return roll_back(FLOUR_ERR_HIP);
+            rc = launch_kv_bundle_copy(1, d_stage, d_pool_ptrs, d_table(), b0, n, num_layers,
+                                       kv_heads, block_size, head_dim, num_slots,
+                                       elem_bytes(dtype), s);
+            if (rc) return roll_back(rc);
+        }
+        if (check_hip(hipStreamSynchronize(s), "kv bundle: import")) return roll_back(FLOUR_ERR_HIP);
+        table.advance((int)tc);
+        // register the imported blocks like a locally computed prefix (cache.rs:323-337)
+        uint64_t parent = PREFIX_SEED;
+        for (int b = 0; b < nb; b++) {
+            const uint32_t* chunk = m.token_ids.data() + (int64_t)b * bs;
+            const uint64_t h = block_hash(parent, chunk, bs);
+            if (!registry.contains(h)) {
+                const int id = table.block_at(b);
+                allocator.incref(id);
+                registry.insert(h, chunk, bs, id);
+            }
+            parent = h;
+        }
+        *imported = (int)tc;
+        return FLOUR_OK;
     }
 };
 
@@ -602,6 +855,23 @@ extern "C" int flour_kv_cache_clear_prefix_cache(flour_kv_cache* c) {
     FLOUR_NEED(c, "kv_cache: null");
     c->c.clear_prefix_cache();
     return FLOUR_OK;
+}
+extern "C" int flour_kv_cache_export_bundle(flour_kv_cache* c, const char* model_id,
+                                            const uint32_t* token_ids, int n_ids, int token_count,
+                                            void* out, size_t cap, size_t* len, void* stream) {
+    clear_error();
+    FLOUR_NEED(c && len, "kv_cache: bad arguments");
+    return c->c.export_bundle(model_id, token_ids, n_ids, token_count, out, cap, len,
+                              static_cast<hipStream_t>(stream));
+}
+extern "C" int flour_kv_cache_import_bundle(flour_kv_cache* c, const void* bytes, size_t len,
+                                            const uint32_t* prompt_tokens, int n_prompt,
+                                            int* imported, void* stream) {
+    clear_error();
+    FLOUR_NEED(c && imported, "kv_cache: bad arguments");
+    *imported = 0;
+    return c->c.import_bundle(bytes, len, prompt_tokens, n_prompt, imported,
+                              static_cast<hipStream_t>(stream));
 }
 extern "C" int flour_kv_cache_pool(const flour_kv_cache* c, int layer, void** k_pool,
                                    void** v_pool, int64_t* num_slots) {

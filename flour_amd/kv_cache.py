@@ -7,7 +7,8 @@ with the same method names and meaning:
 * ``BlockTable``      <- paged.rs:57-121 (slot(pos) = blocks[pos // bs] * bs + pos % bs)
 * ``KvCache``         <- cache.rs KvCache + Cache: allocate_kv, write_kv, attention
   (= kv_blocks + paged_attention), reset_sequence, match_prefix, register_prefix,
-  clear_prefix_cache, free_blocks, with the per-layer pools of PagedKvPool::new on the device.
+  clear_prefix_cache, free_blocks, export_prefix_bundle / import_prefix_bundle (the FLKV
+  frame of src/kv_cache/bundle.rs), with the per-layer pools of PagedKvPool::new on the device.
 
 Every operation is one call into libflour_hip.so; errors raise ``FlourError`` with the
 library's message (the reference's ``candle_core::Error::Msg``).
@@ -130,6 +131,7 @@ class KvCache:
         self.num_layers, self.max_seq_len = num_layers, max_seq_len
         self.num_heads, self.kv_heads, self.head_dim = num_heads, kv_heads, head_dim
         self.block_size, self.dtype = block_size, dtype
+        self.device_pool = bool(device_pool)
         self._h = ctypes.c_void_p()
         from .ops import dtype_code
 
@@ -189,6 +191,38 @@ class KvCache:
 
     def clear_prefix_cache(self) -> None:
         check(lib().flour_kv_cache_clear_prefix_cache(self._h))
+
+    # ---- FLKV bundles (cache.rs:166-340, src/kv_cache/bundle.rs)
+    def export_prefix_bundle(self, model_id: str, token_ids, token_count: int) -> bytes:
+        """Cache::export_prefix_bundle + KvBundleCodec::encode: the FLKV frame of the first
+        token_count live tokens, read from the device pools."""
+        arr, ptr, n = _tokens(token_ids)
+        mid = model_id.encode("utf-8")
+        stream = self._bundle_stream()
+        size = ctypes.c_size_t(0)
+        check(lib().flour_kv_cache_export_bundle(self._h, mid, ptr, n, token_count, None, 0,
+                                                 ctypes.byref(size), stream))
+        buf = ctypes.create_string_buffer(size.value)
+        check(lib().flour_kv_cache_export_bundle(self._h, mid, ptr, n, token_count, buf,
+                                                 size.value, ctypes.byref(size), stream))
+        return buf.raw[:size.value]
+
+    def import_prefix_bundle(self, bundle: bytes, prompt_tokens) -> int:
+        """KvBundleCodec::decode + Cache::import_prefix_bundle; returns the imported token
+        count."""
+        arr, ptr, n = _tokens(prompt_tokens)
+        got = ctypes.c_int(0)
+        check(lib().flour_kv_cache_import_bundle(self._h, bundle, len(bundle), ptr, n,
+                                                 ctypes.byref(got), self._bundle_stream()))
+        return got.value
+
+    def _bundle_stream(self):
+        """torch's current stream for a device pool; none for bookkeeping-only caches."""
+        if not self.device_pool:
+            return None
+        from .ops import _stream
+
+        return _stream()
 
     # ---- device side
     def pool(self, layer: int):

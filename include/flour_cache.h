@@ -12,6 +12,8 @@
  *   src/models/common/cache.rs:13-165   KvCache (allocate, write_current, gather_blocks,
  *                                       reset_sequence, match_prefix, register_prefix)
  *   src/models/common/cache.rs:429-505  Cache::allocate_kv / write_kv / kv_blocks / ...
+ *   src/models/common/cache.rs:166-340  export_prefix_bundle / import_prefix_bundle, with the
+ *   src/kv_cache/bundle.rs:1-214        FLKV frame of KvBundleCodec::encode / decode
  *
  * and replaces the `kv_blocks` + `paged_attention` pair of the attention layer
  * (src/models/common/attention.rs:104-109) by one call that marshals the block table to the
@@ -119,6 +121,35 @@ int flour_kv_cache_match_prefix(flour_kv_cache* c, const uint32_t* tokens, int n
 int flour_kv_cache_register_prefix(flour_kv_cache* c, const uint32_t* tokens, int n);
 /* KvCache::clear_prefix_cache (cache.rs:354-359). */
 int flour_kv_cache_clear_prefix_cache(flour_kv_cache* c);
+
+/* ---- FLKV bundles (src/kv_cache/bundle.rs:1-22, cache.rs:166-340) ----------------------
+ * Frame: "FLKV", version u16 LE = 1, header_len u32 LE, the KvBundleMeta header as serde_json
+ * writes it (fields model_id, token_count, token_ids, block_size, num_layers, num_kv_heads,
+ * head_dim, dtype "F32"/"F16"/"BF16"), then per logical block, per layer, the K block and the V
+ * block, each (kv_heads, block_size, head_dim) little-endian in the pool dtype. */
+
+/* Cache::export_prefix_bundle (cache.rs:166-229) + KvBundleCodec::encode (bundle.rs:108-143):
+ * the frame of the first token_count live tokens, read from the device pools on `stream`.
+ * token_count must be a positive multiple of block_size and at most the live length, and
+ * token_ids must hold at least token_count ids (the reference's error messages, as
+ * FLOUR_ERR_INVALID_ARGUMENT). *len receives the frame size; with out == NULL nothing else
+ * is done (size query), otherwise out (host memory) must hold cap >= *len bytes
+ * (FLOUR_ERR_CAPACITY) and the call returns once it is filled. */
+int flour_kv_cache_export_bundle(flour_kv_cache* c, const char* model_id,
+                                 const uint32_t* token_ids, int n_ids, int token_count, void* out,
+                                 size_t cap, size_t* len, void* stream);
+
+/* KvBundleCodec::decode (bundle.rs:145-214) + Cache::import_prefix_bundle (cache.rs:238-340):
+ * validates the frame (magic, version, header, block alignment, payload length) and the bundle
+ * against this cache (block size, layers, kv heads, head_dim, dtype) and the prompt (it must
+ * start with the bundle's token ids), then resets the sequence, allocates one block per bundle
+ * block, copies the payload into the device pools on `stream`, sets the live length to the
+ * bundle's token count and registers the blocks as a cached prefix. *imported receives the
+ * token count. Rejections leave no partial state; "not enough free kv blocks to import" is
+ * FLOUR_ERR_OUT_OF_BLOCKS (the sequence has been reset, as in the reference). */
+int flour_kv_cache_import_bundle(flour_kv_cache* c, const void* bytes, size_t len,
+                                 const uint32_t* prompt_tokens, int n_prompt, int* imported,
+                                 void* stream);
 
 /* Device pools of one layer (PagedKvPool::block_view, paged.rs:266-279: slot s of kv head h is
  * row h * num_slots + s of each array). */
