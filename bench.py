@@ -147,6 +147,77 @@ def cpu_decode_baseline(case, seconds: float):
     return med, threads, len(times)
 
 
+BUNDLE = dict(num_layers=32, kv_heads=8, head_dim=128, block_size=16, prefix=1024)
+
+
+def bench_bundle(torch, steps: int, warmup: int, cpu: bool):
+    """FLKV export / import of a 1,024-token prefix of a Llama-3-8B-shaped cache (32 layers,
+    8 kv heads, head_dim 128, bf16): the frame is 134 MB. Export = device gather into staging +
+    device-to-host copy into the caller's buffer; import = host-to-device copy + scatter into
+    freshly allocated blocks + bookkeeping. Both end with a stream synchronisation, so the wall
+    time is the host-visible one."""
+    from flour_amd.kv_cache import KvCache
+
+    c = BUNDLE
+    P, dev = c["prefix"], torch.device("cuda:0")
+    mk = lambda: KvCache(c["num_layers"], P + 64, 32, c["kv_heads"], c["head_dim"],  # noqa: E731
+                         torch.bfloat16, c["block_size"])
+    a, b = mk(), mk()
+    a.allocate_kv(P)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    for layer in range(c["num_layers"]):
+        kv = torch.randn((2, P, c["kv_heads"], c["head_dim"]), generator=g).to(torch.bfloat16).to(dev)
+        a.write_kv(layer, kv[0], kv[1])
+    torch.cuda.synchronize()
+    ids = list(range(P))
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        t = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        return t[len(t) // 2]
+
+    # frames live in pinned host buffers, as a serving process would keep them for transfer
+    n = a.bundle_size("llama3-8b", ids, P)
+    buf = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    assert a.export_prefix_bundle("llama3-8b", ids, P, out=buf) == n
+    t_exp = timed(lambda: a.export_prefix_bundle("llama3-8b", ids, P, out=buf))
+    # each import registers its blocks as a cached prefix; drop that before the next one
+    t_imp = timed(lambda: (b.clear_prefix_cache(), b.import_prefix_bundle(buf, ids)))
+    data = bytes(buf.numpy())
+    r = {"bytes": n, "export_GB/s": round(n / t_exp / 1e9, 2),
+         "export_ms": round(t_exp * 1e3, 3), "import_GB/s": round(n / t_imp / 1e9, 2),
+         "import_ms": round(t_imp * 1e3, 3), "host_buffer": "pinned"}
+    b.clear_prefix_cache()
+    b.import_prefix_bundle(buf, ids)
+    assert b.export_prefix_bundle("llama3-8b", ids, P) == data  # the frame survives the trip
+    if cpu:
+        import numpy as np
+
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import flkv as F  # noqa: E402
+
+        pools = [[p.cpu().view(torch.int16).numpy().view(np.uint16) for p in a.pool(layer)]
+                 for layer in range(c["num_layers"])]
+        ks, vs = [p[0] for p in pools], [p[1] for p in pools]
+        blocks = a.blocks()
+        t = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            F.export_frame("llama3-8b", ids, P, ks, vs, blocks, c["block_size"], "BF16")
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        r["cpu_export_GB/s"] = round(n / t[1] / 1e9, 3)
+        r["cpu_sample"] = ("the oracle's export (numpy gather of the host pool copies + frame "
+                           "encoding), whole bundle, median of 3, 1 thread")
+    return r
+
+
 def cpu_rope_baseline(case, theta: float):
     """Oracle RoPE + KV write over the whole batch on host copies; (median seconds, runs)."""
     import numpy as np
@@ -363,6 +434,16 @@ def main():
 
     dev = torch.device("cuda:0")
     name = args.workload
+    if name == "kv_bundle_llama3_8b":
+        r = bench_bundle(torch, args.steps, args.warmup, not args.no_cpu)
+        print(json.dumps({"metric": "FLKV bundle export throughput (frame bytes, host-visible)",
+                          "value": r["export_GB/s"], "unit": "GB/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["export_ms"], "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic (seeded N(0,1) K/V)",
+                          "config": dict(BUNDLE, workload=name), "bundle": r}), flush=True)
+        return
     cfg = WORKLOADS[name]
     case = make_workload(name, device=dev)
     torch.cuda.synchronize()
@@ -446,6 +527,8 @@ def main():
                 extra[nm] = e
             del cs
             torch.cuda.empty_cache()
+        extra["kv_bundle_llama3_8b"] = bench_bundle(torch, 5, 2, not args.no_cpu)
+        torch.cuda.empty_cache()
         result["extra"] = extra
 
     print(json.dumps(result), flush=True)

@@ -193,26 +193,45 @@ class KvCache:
         check(lib().flour_kv_cache_clear_prefix_cache(self._h))
 
     # ---- FLKV bundles (cache.rs:166-340, src/kv_cache/bundle.rs)
-    def export_prefix_bundle(self, model_id: str, token_ids, token_count: int) -> bytes:
+    def export_prefix_bundle(self, model_id: str, token_ids, token_count: int, out=None):
         """Cache::export_prefix_bundle + KvBundleCodec::encode: the FLKV frame of the first
-        token_count live tokens, read from the device pools."""
+        token_count live tokens, read from the device pools. Returns ``bytes``; with ``out`` (a
+        CPU uint8 tensor, pinned for full copy speed, at least bundle_size() bytes) the frame
+        is written there and its length returned."""
         arr, ptr, n = _tokens(token_ids)
         mid = model_id.encode("utf-8")
         stream = self._bundle_stream()
         size = ctypes.c_size_t(0)
         check(lib().flour_kv_cache_export_bundle(self._h, mid, ptr, n, token_count, None, 0,
                                                  ctypes.byref(size), stream))
-        buf = ctypes.create_string_buffer(size.value)
-        check(lib().flour_kv_cache_export_bundle(self._h, mid, ptr, n, token_count, buf,
-                                                 size.value, ctypes.byref(size), stream))
-        return buf.raw[:size.value]
+        if out is None:
+            buf = ctypes.create_string_buffer(size.value)
+            check(lib().flour_kv_cache_export_bundle(self._h, mid, ptr, n, token_count, buf,
+                                                     size.value, ctypes.byref(size), stream))
+            return buf.raw[:size.value]
+        check(lib().flour_kv_cache_export_bundle(self._h, mid, ptr, n, token_count,
+                                                 ctypes.c_void_p(out.data_ptr()), out.numel(),
+                                                 ctypes.byref(size), stream))
+        return size.value
 
-    def import_prefix_bundle(self, bundle: bytes, prompt_tokens) -> int:
-        """KvBundleCodec::decode + Cache::import_prefix_bundle; returns the imported token
-        count."""
+    def bundle_size(self, model_id: str, token_ids, token_count: int) -> int:
+        """Length of the frame export_prefix_bundle would produce."""
+        arr, ptr, n = _tokens(token_ids)
+        size = ctypes.c_size_t(0)
+        check(lib().flour_kv_cache_export_bundle(self._h, model_id.encode("utf-8"), ptr, n,
+                                                 token_count, None, 0, ctypes.byref(size), None))
+        return size.value
+
+    def import_prefix_bundle(self, bundle, prompt_tokens) -> int:
+        """KvBundleCodec::decode + Cache::import_prefix_bundle; ``bundle`` is ``bytes`` or a CPU
+        uint8 tensor (the first ``numel`` bytes). Returns the imported token count."""
         arr, ptr, n = _tokens(prompt_tokens)
         got = ctypes.c_int(0)
-        check(lib().flour_kv_cache_import_bundle(self._h, bundle, len(bundle), ptr, n,
+        if isinstance(bundle, (bytes, bytearray)):
+            data, size = bundle, len(bundle)
+        else:
+            data, size = ctypes.c_void_p(bundle.data_ptr()), bundle.numel()
+        check(lib().flour_kv_cache_import_bundle(self._h, data, size, ptr, n,
                                                  ctypes.byref(got), self._bundle_stream()))
         return got.value
 
