@@ -82,6 +82,25 @@ SIGNATURES: dict[str, tuple] = {
                                               ctypes.POINTER(ctypes.c_size_t), _vp]),
     "flour_kv_cache_import_bundle": (_c_int, [_vp, _vp, _c_sz, _vp, _c_int,
                                               ctypes.POINTER(ctypes.c_int), _vp]),
+    "flour_kv_batch_create": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                       _c_int, _c_int, _c_int, _c_int, _vp]),
+    "flour_kv_batch_destroy": (None, [_vp]),
+    "flour_kv_batch_add_sequence": (_c_int, [_vp, ctypes.POINTER(ctypes.c_int)]),
+    "flour_kv_batch_remove_sequence": (_c_int, [_vp, _c_int]),
+    "flour_kv_batch_reset_sequence": (_c_int, [_vp, _c_int]),
+    "flour_kv_batch_allocate_kv": (_c_int, [_vp, _c_int, _c_int]),
+    "flour_kv_batch_len": (_c_int, [_vp, _c_int]),
+    "flour_kv_batch_free_blocks": (_c_int, [_vp]),
+    "flour_kv_batch_ref_count": (_c_int, [_vp, _c_int]),
+    "flour_kv_batch_blocks": (_c_int, [_vp, _c_int, _vp, _c_int, ctypes.POINTER(ctypes.c_int)]),
+    "flour_kv_batch_match_prefix": (_c_int, [_vp, _c_int, _vp, _c_int]),
+    "flour_kv_batch_register_prefix": (_c_int, [_vp, _c_int, _vp, _c_int]),
+    "flour_kv_batch_clear_prefix_cache": (_c_int, [_vp]),
+    "flour_kv_batch_plan": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "flour_kv_batch_write_kv": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_i64, _vp]),
+    "flour_kv_batch_attention": (_c_int, [_vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _c_int,
+                                          _c_i64, _c_i64, _c_f, _vp]),
+    "flour_kv_batch_pool": (_c_int, [_vp, _c_int, _vp, _vp, _vp]),
     "flour_kv_cache_pool": (_c_int, [_vp, _c_int, _vp, _vp, _vp]),
 }
 

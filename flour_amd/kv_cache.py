@@ -5,6 +5,8 @@ with the same method names and meaning:
 
 * ``BlockAllocator``  <- paged.rs:7-54   (LIFO free list, refcounts; allocate() -> id or None)
 * ``BlockTable``      <- paged.rs:57-121 (slot(pos) = blocks[pos // bs] * bs + pos % bs)
+* ``KvBatch``         <- many sequences over one pool (continuous batching; the reference's
+  engine is batch-1, engine.rs:88, :219-263), one plan per forward step
 * ``KvCache``         <- cache.rs KvCache + Cache: allocate_kv, write_kv, attention
   (= kv_blocks + paged_attention), reset_sequence, match_prefix, register_prefix,
   clear_prefix_cache, free_blocks, export_prefix_bundle / import_prefix_bundle (the FLKV
@@ -286,6 +288,123 @@ class KvCache:
                                              out.stride(2), out.stride(1), float(scale),
                                              _stream()))
         return out
+
+
+class KvBatch:
+    """Many sequences over one device pool (the flour_kv_batch_* calls): a shared
+    BlockAllocator and prefix registry, one BlockTable per sequence, and one plan per forward
+    step that every layer's write_kv / attention uses."""
+
+    def __init__(self, num_layers: int, num_blocks: int, max_seqs: int, max_seq_len: int,
+                 max_batch_tokens: int, num_heads: int, kv_heads: int, head_dim: int, dtype=None,
+                 block_size: int = 16, device_pool: bool = True):
+        import torch
+
+        from .ops import dtype_code
+
+        self.dtype = dtype or torch.bfloat16
+        self.num_layers, self.num_heads, self.kv_heads = num_layers, num_heads, kv_heads
+        self.head_dim, self.block_size = head_dim, block_size
+        self.device_pool = bool(device_pool)
+        self._h = ctypes.c_void_p()
+        check(lib().flour_kv_batch_create(num_layers, num_blocks, max_seqs, max_seq_len,
+                                          max_batch_tokens, num_heads, kv_heads, head_dim,
+                                          block_size, dtype_code(self.dtype), int(device_pool),
+                                          ctypes.byref(self._h)))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().flour_kv_batch_destroy(self._h)
+            self._h = None
+
+    def _r(self, rc: int) -> int:
+        if rc < 0:
+            check(rc)
+        return rc
+
+    def add_sequence(self) -> int:
+        sid = ctypes.c_int(-1)
+        check(lib().flour_kv_batch_add_sequence(self._h, ctypes.byref(sid)))
+        return sid.value
+
+    def remove_sequence(self, sid: int) -> None:
+        check(lib().flour_kv_batch_remove_sequence(self._h, sid))
+
+    def reset_sequence(self, sid: int) -> None:
+        check(lib().flour_kv_batch_reset_sequence(self._h, sid))
+
+    def allocate_kv(self, sid: int, seq_len: int) -> None:
+        check(lib().flour_kv_batch_allocate_kv(self._h, sid, seq_len))
+
+    def len(self, sid: int) -> int:
+        return self._r(lib().flour_kv_batch_len(self._h, sid))
+
+    def free_blocks(self) -> int:
+        return self._r(lib().flour_kv_batch_free_blocks(self._h))
+
+    def ref_count(self, block_id: int) -> int:
+        return self._r(lib().flour_kv_batch_ref_count(self._h, block_id))
+
+    def blocks(self, sid: int) -> list[int]:
+        n = ctypes.c_int(0)
+        check(lib().flour_kv_batch_blocks(self._h, sid, None, 0, ctypes.byref(n)))
+        buf = _i32(n.value)
+        check(lib().flour_kv_batch_blocks(self._h, sid, buf, n.value, ctypes.byref(n)))
+        return list(buf[:n.value])
+
+    def match_prefix(self, sid: int, token_ids) -> int:
+        arr, ptr, n = _tokens(token_ids)
+        return self._r(lib().flour_kv_batch_match_prefix(self._h, sid, ptr, n))
+
+    def register_prefix(self, sid: int, token_ids) -> None:
+        arr, ptr, n = _tokens(token_ids)
+        check(lib().flour_kv_batch_register_prefix(self._h, sid, ptr, n))
+
+    def clear_prefix_cache(self) -> None:
+        check(lib().flour_kv_batch_clear_prefix_cache(self._h))
+
+    def plan(self, seq_ids, seq_q) -> None:
+        """The step: sequence seq_ids[i] brings its last seq_q[i] live positions as new rows,
+        packed in this order."""
+        from .ops import _stream
+
+        ids = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int32))
+        q = np.ascontiguousarray(np.asarray(seq_q, dtype=np.int32))
+        assert ids.size == q.size
+        check(lib().flour_kv_batch_plan(self._h, ids.ctypes.data_as(ctypes.c_void_p),
+                                        q.ctypes.data_as(ctypes.c_void_p), int(ids.size),
+                                        _stream() if self.device_pool else None))
+
+    def write_kv(self, layer: int, k, v) -> None:
+        """The planned new rows, packed (rows, kv_heads, head_dim) with a unit last stride."""
+        from .ops import _ptr, _stream
+
+        assert k.stride() == v.stride() and k.dtype == v.dtype == self.dtype and k.stride(2) == 1
+        check(lib().flour_kv_batch_write_kv(self._h, layer, _ptr(k), _ptr(v), k.stride(0),
+                                            k.stride(1), _stream()))
+
+    def attention(self, layer: int, q, scale: float, out=None, out_dtype=None):
+        """Attention of the planned rows: q packed (rows, num_heads, head_dim); returns the
+        same shape (decode when every sequence brings one row, varlen prefill otherwise)."""
+        import torch
+        from .ops import _ptr, _stream, dtype_code
+
+        T, H, D = q.shape
+        if out is None:
+            out = torch.empty((T, H, D), dtype=out_dtype or q.dtype, device=q.device)
+        check(lib().flour_kv_batch_attention(self._h, layer, _ptr(q), H, q.stride(0), q.stride(1),
+                                             _ptr(out), dtype_code(out.dtype), out.stride(0),
+                                             out.stride(1), float(scale), _stream()))
+        return out
+
+    def pool(self, layer: int):
+        """(k_pool, v_pool) of a layer as torch views (kv_heads, num_slots, head_dim)."""
+        k, v, ns = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int64()
+        check(lib().flour_kv_batch_pool(self._h, layer, ctypes.byref(k), ctypes.byref(v),
+                                        ctypes.byref(ns)))
+        n = self.kv_heads * ns.value * self.head_dim
+        return tuple(_device_view(p.value, n, self.dtype).view(self.kv_heads, ns.value,
+                                                                self.head_dim) for p in (k, v))
 
 
 def _device_view(addr: int, numel: int, dtype):

@@ -156,6 +156,58 @@ int flour_kv_cache_import_bundle(flour_kv_cache* c, const void* bytes, size_t le
 int flour_kv_cache_pool(const flour_kv_cache* c, int layer, void** k_pool, void** v_pool,
                         int64_t* num_slots);
 
+/* ---- Many sequences over one pool (continuous batching) ------------------------------------
+ * The reference engine serves one sequence at a time (one Mutex<Cache>, src/engine.rs:88, and
+ * the batch-1 loop of engine.rs:219-263). A flour_kv_batch shares one device pool of num_blocks
+ * blocks, one BlockAllocator and one prefix registry among up to max_seqs sequences, each with
+ * its own BlockTable and KvCache's per-sequence operations (cache.rs:13-165, :429-505); a
+ * sequence can reuse the full prefix blocks that another registered. A forward step is planned
+ * once (flour_kv_batch_plan uploads the step's block tables, kv lengths, cu_seqlens and the
+ * slot mapping of the new rows); each layer then calls write_kv and attention on that plan.
+ * Any change to a sequence invalidates the plan. Functions of one batch must not be called
+ * concurrently. */
+typedef struct flour_kv_batch flour_kv_batch;
+
+/* Pools (kv_heads, num_blocks * block_size, head_dim) per layer, zero-filled; table rows of
+ * ceil(max_seq_len / block_size) blocks; up to max_batch_tokens new rows per step; a decode
+ * workspace for max_seqs sequences. device_pool == 0 keeps only the bookkeeping. */
+int flour_kv_batch_create(int num_layers, int num_blocks, int max_seqs, int max_seq_len,
+                          int max_batch_tokens, int num_heads, int kv_heads, int head_dim,
+                          int block_size, int dtype, int device_pool, flour_kv_batch** out);
+void flour_kv_batch_destroy(flour_kv_batch* b);
+/* A new empty sequence (FLOUR_ERR_CAPACITY when max_seqs are live). */
+int flour_kv_batch_add_sequence(flour_kv_batch* b, int* seq_id);
+/* Releases the sequence's blocks (KvCache::reset_sequence) and frees its slot. */
+int flour_kv_batch_remove_sequence(flour_kv_batch* b, int seq_id);
+int flour_kv_batch_reset_sequence(flour_kv_batch* b, int seq_id);
+/* Cache::allocate_kv for one sequence ("paged kv cache overflow", "out of kv blocks"). */
+int flour_kv_batch_allocate_kv(flour_kv_batch* b, int seq_id, int seq_len);
+int flour_kv_batch_len(const flour_kv_batch* b, int seq_id);
+int flour_kv_batch_free_blocks(const flour_kv_batch* b);
+int flour_kv_batch_ref_count(const flour_kv_batch* b, int block_id);
+int flour_kv_batch_blocks(const flour_kv_batch* b, int seq_id, int32_t* out, int cap, int* n);
+/* KvCache::match_prefix into an empty sequence, over the shared registry; returns the matched
+ * token count. */
+int flour_kv_batch_match_prefix(flour_kv_batch* b, int seq_id, const uint32_t* tokens, int n);
+int flour_kv_batch_register_prefix(flour_kv_batch* b, int seq_id, const uint32_t* tokens, int n);
+int flour_kv_batch_clear_prefix_cache(flour_kv_batch* b);
+/* The step: sequence seq_ids[i] brings its last seq_q[i] live positions as new rows (already
+ * allocated), packed in this order (cu_seqlens). Sequences must be distinct. */
+int flour_kv_batch_plan(flour_kv_batch* b, const int* seq_ids, const int* seq_q, int n_seqs,
+                        void* stream);
+/* The KV write of the planned new rows: k/v element (t, h, d) of packed row t at
+ * t*stride_tok + h*stride_head + d (flour_hip_kv_write). */
+int flour_kv_batch_write_kv(flour_kv_batch* b, int layer, const void* k, const void* v,
+                            int64_t stride_tok, int64_t stride_head, void* stream);
+/* Attention of the planned rows: paged decode when every sequence brings one row (q and out
+ * (n_seqs, num_heads, head_dim) contiguous), varlen prefill otherwise (strided packed rows). */
+int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void* q, int num_heads,
+                             int64_t q_stride_tok, int64_t q_stride_head, void* out,
+                             int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,
+                             float scale, void* stream);
+int flour_kv_batch_pool(const flour_kv_batch* b, int layer, void** k_pool, void** v_pool,
+                        int64_t* num_slots);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,92 @@
+"""Many sequences over one pool (flour_kv_batch_*), bookkeeping on the CPU.
+
+Each sequence behaves as the reference's KvCache (cache.rs allocate_kv, reset_sequence,
+match_prefix, register_prefix; paged.rs BlockAllocator LIFO order and refcounts); what is new is
+that the allocator and the prefix registry are shared, so one sequence reuses the full prefix
+blocks another registered, and removing a sequence returns only the blocks nobody else holds.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from flour_amd import _lib
+from flour_amd.kv_cache import KvBatch
+
+
+def batch(num_blocks=8, max_seqs=3, max_seq_len=64, tokens=256):
+    return KvBatch(2, num_blocks, max_seqs, max_seq_len, tokens, 2, 2, 4, torch.float32, 16,
+                   device_pool=False)
+
+
+def test_sequences_share_the_allocator():
+    b = batch()
+    s0, s1 = b.add_sequence(), b.add_sequence()
+    b.allocate_kv(s0, 40)          # 3 blocks; the free list hands out 0, 1, 2 first
+    b.allocate_kv(s1, 17)          # 2 blocks
+    assert b.blocks(s0) == [0, 1, 2] and b.blocks(s1) == [3, 4]
+    assert b.free_blocks() == 3 and b.len(s0) == 40 and b.len(s1) == 17
+    b.remove_sequence(s0)          # LIFO: the last freed block comes back first
+    assert b.free_blocks() == 6
+    s2 = b.add_sequence()
+    assert s2 == s0
+    b.allocate_kv(s2, 1)
+    assert b.blocks(s2) == [2]
+
+
+def test_prefix_shared_across_sequences():
+    b = batch()
+    ids = list(range(40))
+    a = b.add_sequence()
+    b.allocate_kv(a, 40)
+    b.register_prefix(a, ids)      # 2 full blocks registered
+    c = b.add_sequence()
+    assert b.match_prefix(c, ids) == 32
+    assert b.blocks(c) == b.blocks(a)[:2] and b.len(c) == 32
+    assert [b.ref_count(x) for x in b.blocks(a)] == [3, 3, 1]
+    b.remove_sequence(a)           # the registry and c still hold the shared blocks
+    assert [b.ref_count(x) for x in b.blocks(c)] == [2, 2] and b.free_blocks() == 6
+    b.remove_sequence(c)
+    assert b.free_blocks() == 6    # registry-only blocks stay cached
+    b.clear_prefix_cache()
+    assert b.free_blocks() == 8
+    # a block-aligned prompt leaves its last block to compute (cache.rs:112-140)
+    d = b.add_sequence()
+    assert b.match_prefix(d, ids[:32]) == 0
+
+
+def test_errors():
+    b = batch(num_blocks=4, max_seqs=2)
+    s0, s1 = b.add_sequence(), b.add_sequence()
+    with pytest.raises(_lib.FlourError, match="all 2 sequence slots"):
+        b.add_sequence()
+    with pytest.raises(_lib.FlourError, match="paged kv cache overflow"):
+        b.allocate_kv(s0, 65)
+    b.allocate_kv(s0, 48)
+    with pytest.raises(_lib.FlourError, match="out of kv blocks"):
+        b.allocate_kv(s1, 32)
+    with pytest.raises(_lib.FlourError, match="no live sequence 7"):
+        b.allocate_kv(7, 1)
+    with pytest.raises(_lib.FlourError, match="needs an empty sequence"):
+        b.match_prefix(s0, range(48))
+    b.remove_sequence(s1)
+    with pytest.raises(_lib.FlourError, match="no live sequence 1"):
+        b.len(s1)
+
+
+def test_plan_validation():
+    b = batch()
+    s0, s1 = b.add_sequence(), b.add_sequence()
+    b.allocate_kv(s0, 10)
+    b.allocate_kv(s1, 5)
+    with pytest.raises(_lib.FlourError, match="listed twice"):
+        b.plan([s0, s0], [1, 1])
+    with pytest.raises(_lib.FlourError, match="brings 6 new rows over 5"):
+        b.plan([s0, s1], [1, 6])
+    with pytest.raises(_lib.FlourError, match="exceed max_batch_tokens 8"):
+        batch_small = batch(tokens=8)
+        t = batch_small.add_sequence()
+        batch_small.allocate_kv(t, 10)
+        batch_small.plan([t], [10])
+    with pytest.raises(_lib.FlourError, match="no device pool"):
+        b.plan([s0, s1], [10, 5])

@@ -1,0 +1,123 @@
+"""Many sequences over one pool (flour_kv_batch_*) on the GPU, against the oracle.
+
+A step plans the batch once and every layer runs the KV write and attention over it. Each
+sequence's output is checked against the oracle's paged_attention (cpu.rs:57-112) over that
+sequence's own block table in the shared pool: a mixed prefill of sequences of different
+lengths, decode steps for all of them (the paged decode kernel), a shared cached prefix matched
+through the common registry with the suffixes prefilled in one call, and sequences removed and
+added between steps. Tolerances as for the kernels: bf16 max-abs <= 2e-3 and rel-L2 <= 1e-3
+against the fp32 oracle (fp32 output).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _util import errors, to_np
+from flour_amd import _lib
+from flour_amd.kv_cache import KvBatch
+
+pytestmark = pytest.mark.gpu
+
+H, G, D, BS = 16, 4, 128, 16
+SCALE = D ** -0.5
+
+
+def make(num_blocks=512, max_seqs=8, max_seq_len=1024, tokens=4096, layers=2):
+    return KvBatch(layers, num_blocks, max_seqs, max_seq_len, tokens, H, G, D, torch.bfloat16, BS)
+
+
+def rows(n, g, scale=1.0):
+    return (torch.randn((n, G, D), generator=g) * scale).to(torch.bfloat16).cuda()
+
+
+def step(b, layer, sids, qn, g):
+    """Plan, write new K/V rows, attend: returns (q, out) packed in plan order."""
+    b.plan(sids, qn)
+    T = sum(qn)
+    k, v = rows(T, g), rows(T, g)
+    b.write_kv(layer, k, v)
+    q = torch.randn((T, H, D), generator=g).to(torch.bfloat16).cuda()
+    out = b.attention(layer, q, SCALE, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    return q, out
+
+
+def check(b, layer, sids, qn, q, out, tag):
+    kp, vp = (to_np(t) for t in b.pool(layer))
+    mb = max(len(b.blocks(s)) for s in sids)
+    bt = np.zeros((len(sids), mb), np.int32)
+    for i, s in enumerate(sids):
+        bl = b.blocks(s)
+        bt[i, :len(bl)] = bl
+    cu = np.concatenate([[0], np.cumsum(qn)]).astype(np.int32)
+    kl = np.array([b.len(s) for s in sids], np.int32)
+    ref = O.paged_attention(to_np(q), kp, vp, bt, cu, kl, BS, SCALE, bf16=True)
+    max_abs, rel = errors(to_np(out), ref)
+    print(f"{tag}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+def test_mixed_prefill_then_decode_steps(device):
+    g = torch.Generator(device="cpu").manual_seed(1)
+    b = make()
+    lens = [300, 17, 1, 129, 512, 64]
+    sids = [b.add_sequence() for _ in lens]
+    for s, n in zip(sids, lens):
+        b.allocate_kv(s, n)
+    for layer in range(2):
+        q, out = step(b, layer, sids, lens, g)
+        check(b, layer, sids, lens, q, out, f"prefill layer {layer}")
+    for t in range(3):  # decode steps: one new row per sequence, the paged decode kernel
+        for s in sids:
+            b.allocate_kv(s, 1)
+        for layer in range(2):
+            q, out = step(b, layer, sids, [1] * len(sids), g)
+            check(b, layer, sids, [1] * len(sids), q, out, f"decode {t} layer {layer}")
+
+
+def test_shared_prefix_through_the_registry(device):
+    """One sequence computes and registers a 256-token prefix; five more match it from the
+    shared registry (same physical blocks) and prefill their own suffixes in one call."""
+    g = torch.Generator(device="cpu").manual_seed(2)
+    b = make()
+    prefix = list(range(1000, 1256))
+    s0 = b.add_sequence()
+    assert b.match_prefix(s0, prefix + [1]) == 0
+    b.allocate_kv(s0, 256 + 1)
+    step(b, 0, [s0], [257], g)
+    b.register_prefix(s0, prefix + [1])
+    shared = b.blocks(s0)[:16]
+    others, suffix = [], [33, 1, 200, 77, 128]
+    for n in suffix:
+        s = b.add_sequence()
+        assert b.match_prefix(s, prefix + list(range(n))) == 256
+        assert b.blocks(s) == shared
+        b.allocate_kv(s, n)
+        others.append(s)
+    assert all(b.ref_count(x) == 7 for x in shared)  # s0, the registry and five sequences
+    q, out = step(b, 0, others, suffix, g)
+    check(b, 0, others, suffix, q, out, "suffixes over the shared prefix")
+
+
+def test_sequences_leave_and_join_between_steps(device):
+    g = torch.Generator(device="cpu").manual_seed(3)
+    b = make(num_blocks=64)
+    sids = [b.add_sequence() for _ in range(4)]
+    for s in sids:
+        b.allocate_kv(s, 100)
+    step(b, 0, sids, [100] * 4, g)
+    free = b.free_blocks()
+    b.remove_sequence(sids[1])
+    assert b.free_blocks() == free + 7
+    s_new = b.add_sequence()
+    assert s_new == sids[1]
+    b.allocate_kv(s_new, 40)
+    live = [sids[0], s_new, sids[2], sids[3]]
+    q, out = step(b, 0, live, [1, 40, 1, 1], g)  # decode rows and a new prefill together
+    check(b, 0, live, [1, 40, 1, 1], q, out, "after churn")
+    b.allocate_kv(sids[0], 1)
+    with pytest.raises(_lib.FlourError, match="no current plan"):
+        b.write_kv(0, rows(1, g), rows(1, g))
