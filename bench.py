@@ -16,6 +16,10 @@ stream) against the 8 TB/s HBM peak; `cpu_baseline` is the repo's C restatement 
 reference CPU backend (oracle/) timed on this host's cores on a bounded sample of the same
 workload. `extra` carries the other workloads (prefill TFLOP/s against the 2.5 PFLOP/s dense
 bf16 peak, long-context decode, KV write) measured the same way.
+
+Consecutive timed launches rotate over copies of the large inputs (pools, new rows, q), at
+least 1 GiB per rotation, so every launch reads from HBM rather than from the 256 MB
+Infinity Cache that a re-read of the same 577 MB pool would partly hit.
 """
 from __future__ import annotations
 
@@ -103,6 +107,30 @@ def loop_timed(torch, fn, steps: int, warmup: int) -> float:
     t1.record()
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / steps
+
+
+# Every timed launch reads inputs that no launch of the previous ~1 GiB touched: a step
+# re-reading the same pools would be served partly by the 256 MB Infinity Cache (measured: the
+# Llama-3-8B decode reads 5.76 TB/s from one resident copy, 5.23 TB/s rotating over two or
+# more), which is not HBM throughput.
+COLD_BYTES = 1 << 30
+
+
+def cold_copies(per_copy_bytes: int) -> int:
+    """Copies of a step's large inputs so that one rotation touches >= COLD_BYTES (2..16)."""
+    return int(max(2, min(16, -(-COLD_BYTES // max(1, per_copy_bytes)))))
+
+
+def rotating(fns):
+    """A callable that runs fns[0], fns[1], ... in turn, one per call."""
+    state = {"i": 0}
+
+    def run():
+        f = fns[state["i"] % len(fns)]
+        state["i"] += 1
+        f()
+
+    return run
 
 
 def read_traffic(name: str):
@@ -218,6 +246,91 @@ def bench_bundle(torch, steps: int, warmup: int, cpu: bool):
     return r
 
 
+BATCH_DECODE = dict(num_layers=32, batch=64, num_heads=32, kv_heads=8, head_dim=128,
+                    block_size=16, ctx=(512, 4096), seed=2)
+
+
+def bench_batch_decode(torch, steps: int, warmup: int, cpu: bool, cpu_seconds: float):
+    """Continuous-batching decode over a Llama-3-8B-shaped cache (32 layers, 32 q / 8 kv heads,
+    head_dim 128, bf16, block 16): 64 sequences with the decode workload's seeded contexts
+    U[512, 4096] live in one KvBatch pool. A step is one flour_kv_batch_step (one new row per
+    sequence: allocation + plan upload) and, for each of the 32 layers, the KV write of the 64
+    new rows and paged decode attention over the whole batch. `kernels_ms` times the same 64
+    launches with no step call between them, so step_ms - kernels_ms is the host share."""
+    import types
+
+    from flour_amd.kv_cache import KvBatch
+
+    c = BATCH_DECODE
+    L, B, H, G, D, bs = (c[k] for k in ("num_layers", "batch", "num_heads", "kv_heads",
+                                        "head_dim", "block_size"))
+    g = torch.Generator(device="cpu").manual_seed(c["seed"])
+    ctx = torch.randint(c["ctx"][0], c["ctx"][1] + 1, (B,), generator=g).tolist()
+    grow = 2 * (warmup + steps) + 2
+    max_len = -(-(c["ctx"][1] + grow) // bs) * bs
+    nblk = sum(-(-(n + grow) // bs) for n in ctx) + B
+    b = KvBatch(L, nblk, B, max_len, B, H, G, D, torch.bfloat16, bs)
+    torch.manual_seed(c["seed"] + 1000)
+    for layer in range(L):
+        for p in b.pool(layer):
+            p.normal_()
+    sids = [b.add_sequence() for _ in range(B)]
+    for s, n in zip(sids, ctx):
+        b.allocate_kv(s, n - 1)    # the first step brings row n
+    dev = torch.device("cuda:0")
+    q = torch.randn((L, B, H, D), device=dev).to(torch.bfloat16)
+    k = torch.randn((L, B, G, D), device=dev).to(torch.bfloat16)
+    v = torch.randn((L, B, G, D), device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    ones, scale = [1] * B, D ** -0.5
+    torch.cuda.synchronize()
+
+    def layers():
+        for layer in range(L):
+            b.write_kv(layer, k[layer], v[layer])
+            b.attention(layer, q[layer], scale, out=out[layer])
+
+    def step():
+        b.step(sids, ones)
+        layers()
+
+    t0 = sum(b.len(s) for s in sids)
+    step_ms = loop_timed(torch, step, steps, warmup)
+    t1 = sum(b.len(s) for s in sids)
+    kern_ms = loop_timed(torch, layers, steps, warmup)
+    # mean live rows over the timed steps (each step adds one row per sequence)
+    rows = t1 - B * (steps - 1) / 2.0
+    nb = sum(len(b.blocks(s)) for s in sids)
+    per_layer = rows * G * D * 2 * 2 + B * H * D * 2 * 2 + nb * 4 + B * 4 + (B * G * D * 2 * 2 * 2 + B * 4)
+    nbytes = int(L * per_layer)
+    assert t1 - t0 == B * (warmup + steps)
+    r = {"sequences": B, "layers": L, "step_ms": round(step_ms, 4),
+         "kernels_ms": round(kern_ms, 4),
+         "host_share": round(max(0.0, step_ms - kern_ms) / step_ms, 4),
+         "tokens/s": round(B / (step_ms * 1e-3), 1), "algorithmic_bytes": nbytes,
+         "GB/s": round(nbytes / (step_ms * 1e-3) / 1e9, 1),
+         "hbm_frac": round(nbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if cpu:
+        mb = max(len(b.blocks(s)) for s in sids)
+        bt = torch.zeros((B, mb), dtype=torch.int32)
+        for i, s in enumerate(sids):
+            bl = b.blocks(s)
+            bt[i, :len(bl)] = torch.tensor(bl, dtype=torch.int32)
+        kp, vp = b.pool(0)
+        case = types.SimpleNamespace(q=q[0], k_pool=kp, v_pool=vp, block_tables=bt,
+                                     context_lens=torch.tensor([b.len(s) for s in sids],
+                                                               dtype=torch.int32),
+                                     block_size=bs, scale=scale)
+        med, threads, reps = cpu_decode_baseline(case, cpu_seconds)
+        r["cpu_tokens/s"] = round(B / (med * L), 2)
+        r["cpu_sample"] = (f"one layer of the batch (64 sequences, C restatement of cpu.rs:57-112, "
+                           f"{threads} threads, median of {reps}), x{L} layers; the KV write and "
+                           "bookkeeping not counted")
+        r["speedup"] = round(r["tokens/s"] / r["cpu_tokens/s"], 1)
+    del b
+    return r
+
+
 def cpu_rope_baseline(case, theta: float):
     """Oracle RoPE + KV write over the whole batch on host copies; (median seconds, runs)."""
     import numpy as np
@@ -291,31 +404,39 @@ def bench_decode(torch, ops, case, steps, warmup, graph: bool = False):
     the kernels and their arguments are the same as in the eager call."""
     ws = ops.DecodeWorkspace(case.q.device)
     out = torch.empty_like(case.q)
+    n = cold_copies(case.k_pool.nbytes + case.v_pool.nbytes)
+    kps = [case.k_pool] + [case.k_pool.clone() for _ in range(n - 1)]
+    vps = [case.v_pool] + [case.v_pool.clone() for _ in range(n - 1)]
 
-    def step():
-        ops.paged_decode(case.q, case.k_pool, case.v_pool, case.block_tables, case.context_lens,
+    def step(i):
+        ops.paged_decode(case.q, kps[i], vps[i], case.block_tables, case.context_lens,
                          case.scale, case.max_context_len, block_size=case.block_size, out=out,
                          workspace=ws)
 
-    run = ops.prepare_paged_decode(case.q, case.k_pool, case.v_pool, case.block_tables,
-                                   case.context_lens, case.scale, case.max_context_len, out, ws,
-                                   block_size=case.block_size)
+    runs = [ops.prepare_paged_decode(case.q, kps[i], vps[i], case.block_tables,
+                                     case.context_lens, case.scale, case.max_context_len, out, ws,
+                                     block_size=case.block_size) for i in range(n)]
     if graph:
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(2):
-                step()  # sizes the workspace before capture
+                step(0)  # sizes the workspace before capture
         torch.cuda.current_stream().wait_stream(side)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step()
-        run = g.replay
+        graphs = []
+        for i in range(n):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step(i)
+            graphs.append(g)
+        runs = [g.replay for g in graphs]
+    run = rotating(runs)
     _, per = event_timed(torch, run, steps, warmup)  # per-launch durations (events per call)
     kern_ms = sum(per) / len(per)
     wall_ms = loop_timed(torch, run, steps, warmup)  # whole-job rate: events only at the ends
     nbytes = case.algorithmic_bytes()
-    return dict(ms_per_step=wall_ms, kernel_ms=kern_ms, bytes=nbytes,
+    del kps, vps, runs
+    return dict(ms_per_step=wall_ms, kernel_ms=kern_ms, bytes=nbytes, copies=n,
                 gbs_step=nbytes / (wall_ms * 1e-3) / 1e9, gbs_kernel=nbytes / (kern_ms * 1e-3) / 1e9)
 
 
@@ -344,35 +465,42 @@ def rope_bytes(case) -> int:
 
 def bench_prefill(torch, ops, case, steps, warmup, theta=500000.0):
     out = torch.empty_like(case.q)
+    big = (case.q, case.k_new, case.v_new, case.k_pool, case.v_pool)
+    n = cold_copies(sum(t.nbytes for t in big))
+    sets = [big] + [tuple(t.clone() for t in big) for _ in range(n - 1)]
 
-    def write():
-        ops.kv_write(case.k_new, case.v_new, case.k_pool, case.v_pool, case.slot_mapping)
+    def write_i(i):
+        _, k, v, kp, vp = sets[i]
+        ops.kv_write(k, v, kp, vp, case.slot_mapping)
 
-    def attn():
-        ops.varlen_prefill(case.q, case.k_pool, case.v_pool, case.cu_seqlens_q, case.kv_lens,
+    def attn_i(i):
+        q, _, _, kp, vp = sets[i]
+        ops.varlen_prefill(q, kp, vp, case.cu_seqlens_q, case.kv_lens,
                            case.block_tables, case.max_seqlen_q, case.scale,
                            block_size=case.block_size, out=out)
 
-    def step():
-        write()
-        attn()
+    def step_i(i):
+        write_i(i)
+        attn_i(i)
 
     pos, cos, sin = rope_inputs(torch, ops, case, theta)
     q_rot = torch.empty_like(case.q)
 
-    def rope():
-        ops.rope_kv_write(case.q, case.k_new, case.v_new, case.k_pool, case.v_pool,
-                          case.slot_mapping, pos, cos, sin, q_out=q_rot)
+    def rope_i(i):
+        q, k, v, kp, vp = sets[i]
+        ops.rope_kv_write(q, k, v, kp, vp, case.slot_mapping, pos, cos, sin, q_out=q_rot)
 
-    wall_ms, _ = event_timed(torch, step, steps, warmup)
-    _, per_w = event_timed(torch, write, steps, 1)
-    _, per_a = event_timed(torch, attn, steps, 1)
-    _, per_r = event_timed(torch, rope, steps, 1)
+    each = lambda f: rotating([(lambda i=i: f(i)) for i in range(n)])  # noqa: E731
+    wall_ms, _ = event_timed(torch, each(step_i), steps, warmup)
+    _, per_w = event_timed(torch, each(write_i), steps, 1)
+    _, per_a = event_timed(torch, each(attn_i), steps, 1)
+    _, per_r = event_timed(torch, each(rope_i), steps, 1)
+    del sets
     w_ms = sum(per_w) / len(per_w)
     a_ms = sum(per_a) / len(per_a)
     r_ms = sum(per_r) / len(per_r)
     flops = case.flops()
-    return dict(ms_per_step=wall_ms, attn_ms=a_ms, write_ms=w_ms, flops=flops,
+    return dict(ms_per_step=wall_ms, attn_ms=a_ms, write_ms=w_ms, flops=flops, copies=n,
                 tflops=flops / (a_ms * 1e-3) / 1e12, write_bytes=case.write_bytes(),
                 write_gbs=case.write_bytes() / (w_ms * 1e-3) / 1e9,
                 causal_pairs=case.causal_pairs(), rope_ms=r_ms, rope_bytes=rope_bytes(case),
@@ -392,7 +520,8 @@ def prefill_line(torch, ops, case, name, cfg, args):
         "config": {"workload": name, "num_seqs": cfg["num_seqs"], "num_heads": cfg["num_heads"],
                    "kv_heads": cfg["kv_heads"], "head_dim": cfg["head_dim"],
                    "block_size": cfg["block_size"], "q_len": f"U[{cfg['q_len'][0]},{cfg['q_len'][1]}]",
-                   "prefix": cfg["prefix"], "flops_per_step": r["flops"]},
+                   "prefix": cfg["prefix"], "flops_per_step": r["flops"],
+                   "input_copies": r["copies"]},
         "roofline": {"bound": "mfma", "kernel": "varlen_prefill_mfma_kernel",
                      "achieved": round(r["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
@@ -444,6 +573,17 @@ def main():
                           "data": "synthetic (seeded N(0,1) K/V)",
                           "config": dict(BUNDLE, workload=name), "bundle": r}), flush=True)
         return
+    if name == "decode_batch_llama3_8b":
+        r = bench_batch_decode(torch, args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
+        print(json.dumps({"metric": "continuous-batching decode steps (64 sequences x 32 layers)",
+                          "value": r["tokens/s"], "unit": "tokens/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["step_ms"], "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic (seeded N(0,1) pools, q, k, v)",
+                          "config": dict(BATCH_DECODE, workload=name), "batch_decode": r}),
+              flush=True)
+        return
     cfg = WORKLOADS[name]
     case = make_workload(name, device=dev)
     torch.cuda.synchronize()
@@ -472,6 +612,7 @@ def main():
             "block_size": cfg["block_size"], "context_lens": f"U[{cfg['ctx'][0]},{cfg['ctx'][1]}]",
             "total_context_tokens": int(case.context_lens.sum().item()),
             "algorithmic_bytes_per_step": r["bytes"], "out_dtype": "bf16",
+            "pool_copies": r["copies"],
             "launch": "HIP graph replay of the step" if args.graph else "eager",
         },
         "roofline": {
@@ -528,6 +669,8 @@ def main():
             del cs
             torch.cuda.empty_cache()
         extra["kv_bundle_llama3_8b"] = bench_bundle(torch, 5, 2, not args.no_cpu)
+        torch.cuda.empty_cache()
+        extra["decode_batch_llama3_8b"] = bench_batch_decode(torch, 10, 3, not args.no_cpu, 3.0)
         torch.cuda.empty_cache()
         result["extra"] = extra
 

@@ -97,6 +97,7 @@ SIGNATURES: dict[str, tuple] = {
     "flour_kv_batch_register_prefix": (_c_int, [_vp, _c_int, _vp, _c_int]),
     "flour_kv_batch_clear_prefix_cache": (_c_int, [_vp]),
     "flour_kv_batch_plan": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "flour_kv_batch_step": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "flour_kv_batch_write_kv": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_i64, _vp]),
     "flour_kv_batch_attention": (_c_int, [_vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _c_int,
                                           _c_i64, _c_i64, _c_f, _vp]),

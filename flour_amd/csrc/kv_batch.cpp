@@ -317,6 +317,55 @@ struct KvBatchImpl {
         plan_max_ctx = max_ctx;
         return FLOUR_OK;
     }
+    // allocate_kv(ids[i], q[i]) for every sequence of the step, then plan(): all checks
+    // (sequences, max_seq_len, max_batch_tokens, free blocks, the device pool) come first, so a
+    // refused step changes no sequence.
+    int step(const int* ids, const int* q, int n, hipStream_t s) {
+        planned = false;
+        if (n < 1 || n > max_seqs || !ids || !q) {
+            set_error("kv_batch: step over %d sequences (1 .. %d)", n, max_seqs);
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        }
+        std::vector<uint8_t> seen(max_seqs, 0);
+        int64_t total = 0, need = 0;
+        for (int i = 0; i < n; i++) {
+            if (int rc = need_live(ids[i])) return rc;
+            if (seen[ids[i]]++) {
+                set_error("kv_batch: sequence %d listed twice in one step", ids[i]);
+                return FLOUR_ERR_INVALID_ARGUMENT;
+            }
+            if (q[i] < 1) {
+                set_error("kv_batch: sequence %d brings %d new rows", ids[i], q[i]);
+                return FLOUR_ERR_INVALID_ARGUMENT;
+            }
+            const BlockTable& t = tables[ids[i]];
+            const int64_t end = (int64_t)t.len() + q[i];
+            if (end > max_seq_len) {
+                set_error("paged kv cache overflow: %lld tokens exceeds max_seq_len %d",
+                          (long long)end, max_seq_len);
+                return FLOUR_ERR_CAPACITY;
+            }
+            need += std::max<int64_t>(0, (end + block_size - 1) / block_size -
+                                             (int64_t)t.blocks().size());
+            total += q[i];
+        }
+        if (total > max_tokens) {
+            set_error("kv_batch: %lld new rows exceed max_batch_tokens %d", (long long)total,
+                      max_tokens);
+            return FLOUR_ERR_CAPACITY;
+        }
+        if (need > allocator.num_free()) {
+            set_error("out of kv blocks");
+            return FLOUR_ERR_OUT_OF_BLOCKS;
+        }
+        if (!device) {
+            set_error("kv_batch: no device pool");
+            return FLOUR_ERR_UNSUPPORTED;
+        }
+        for (int i = 0; i < n; i++)
+            if (int rc = allocate_kv(ids[i], q[i])) return rc;  // cannot fail after the checks
+        return plan(ids, q, n, s);
+    }
     int need_plan(int layer) const {
         if (!planned) {
             set_error("kv_batch: no current plan (plan() after the last change to a sequence)");
@@ -448,6 +497,12 @@ extern "C" int flour_kv_batch_plan(flour_kv_batch* b, const int* seq_ids, const 
     clear_error();
     BATCH_NEED(b, "kv_batch: null");
     return b->b.plan(seq_ids, seq_q, n_seqs, static_cast<hipStream_t>(stream));
+}
+extern "C" int flour_kv_batch_step(flour_kv_batch* b, const int* seq_ids, const int* seq_q,
+                                   int n_seqs, void* stream) {
+    clear_error();
+    BATCH_NEED(b, "kv_batch: null");
+    return b->b.step(seq_ids, seq_q, n_seqs, static_cast<hipStream_t>(stream));
 }
 extern "C" int flour_kv_batch_write_kv(flour_kv_batch* b, int layer, const void* k, const void* v,
                                        int64_t stride_tok, int64_t stride_head, void* stream) {

@@ -21,7 +21,8 @@
 // Inside a piece (bf16/f16 pools, head_dim 128, block_size a multiple of 16):
 //  * The wave walks its piece chunk by chunk. A chunk is two 16-token MFMA tiles, each one
 //    4 KB (head, 16 slots) pool run of K and of V, read with buffer loads (per-pool resource,
-//    loop-invariant lane offset, per-tile SGPR offset; V non-temporal); two register buffers
+//    loop-invariant lane offset, per-tile SGPR offset; non-temporal, whole rows per
+//    instruction; K is turned into the MFMA layout through LDS); two register buffers
 //    ping-pong so the next chunk's loads are in flight while one is computed, with the loop
 //    peeled so that no load is conditional. Every query head of the kv head shares each K/V
 //    load (GQA reuse: K/V leave HBM once).
@@ -60,17 +61,17 @@ static constexpr int DEC_CHUNK = 32;         // tokens per step (two 16-token MF
 static constexpr int DEC_SEG = 32;           // chunks per tile-slot refill (64 tiles, one per lane)
 static constexpr int DEC_MAX_BATCH = 4096;   // per-sequence chunk prefix sums live in LDS
 static constexpr int DEC_WAVES_PER_CU = 8;  // 2 per SIMD: the register budget of the kernel
-// K rows are read as two 64 B halves of each 128 B line by back-to-back instructions; a
-// cached load lets the second half hit the line the first brought in, which measures faster
-// than the non-temporal hint that suits the fully coalesced V rows.
-#ifndef FLOUR_DEC_K_POLICY
-#define FLOUR_DEC_K_POLICY 0
-#endif
-static constexpr int K_POLICY = FLOUR_DEC_K_POLICY;
+// K is read like V, four whole 256 B rows per instruction with the non-temporal hint, and
+// turned into the MFMA A-operand layout (row = lane % 16) through a per-wave LDS tile. Reading
+// K directly in that layout takes a 64 B quarter of 16 rows per instruction, a pattern that
+// streams at most ~6.0 TB/s from HBM against ~6.8 TB/s for whole rows (measured with the same
+// 2048-wave, double-buffered access over random 4 KB runs).
+static constexpr int DEC_KPITCH = 272;  // bytes per K row in LDS: conflict-free writes and reads
 
 struct DecodeWs {
     float* ml;  // [2 * num_waves][n_rep][2] (max, sum) in the exp2 domain
     float* o;   // [2 * num_waves][n_rep][D]
+    int* pre;   // [batch + 1] chunk prefix sums, written by workgroup 0 for the merge kernel
 };
 
 static int g_wg_override = 0;  // tuning / test hook: number of waves (0 = one resident round)
@@ -96,10 +97,11 @@ static int decode_workgroups() {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static size_t decode_ws_bytes(int nwg, int n_rep, int head_dim) {
+static size_t decode_ws_bytes(int nwg, int n_rep, int head_dim, int batch) {
     const size_t slots = 2 * (size_t)nwg;
     return align256(slots * n_rep * 2 * sizeof(float)) +
-           align256(slots * n_rep * (size_t)head_dim * sizeof(float));
+           align256(slots * n_rep * (size_t)head_dim * sizeof(float)) +
+           align256(((size_t)batch + 1) * sizeof(int));
 }
 
 __device__ __forceinline__ int decode_chunks(int ctx, int max_ctx) {
@@ -122,6 +124,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     int block_size, int64_t num_slots, int max_ctx, float scale_log2, DecodeWs ws) {
     constexpr int D = DEC_D;
     extern __shared__ int pre[];  // pre[b] = chunks of sequences 0..b-1; pre[batch] = all
+    __shared__ __attribute__((aligned(16))) unsigned char kt[16 * DEC_KPITCH];  // one K tile
     const int lane = threadIdx.x, lg = lane >> 4, lc = lane & 15;
 
     // ---- exclusive prefix sum of per-sequence chunk counts (each lane scans a slice)
@@ -148,6 +151,8 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
         }
         if (lane == 63) pre[batch] = incl;
         __syncthreads();
+        if (blockIdx.x == 0)  // for the merge kernel (ordered by the kernel boundary)
+            for (int b = lane; b <= batch; b += 64) ws.pre[b] = pre[b];
     }
     const int64_t total = (int64_t)kv_heads * pre[batch];
     const int64_t nwg = gridDim.x, wgi = blockIdx.x;
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     if (lo >= hi) return;
 
     const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
-    const uint32_t k_off = (uint32_t)((lc * D + 8 * lg) * sizeof(T));
+    // K and V: instruction j of a tile reads rows 4lg + j, dims 8lc .. 8lc + 7 (4 whole rows)
     const uint32_t v_off = (uint32_t)((4 * lg * D + 8 * lc) * sizeof(T));
     const int64_t max_phys = num_slots / block_size - 1;
 
@@ -211,9 +216,9 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
             const uint32_t soff =
                 (uint32_t)__builtin_amdgcn_readlane(slots, tile0 + t) * (uint32_t)(D * sizeof(T));
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-                kd[t][kk] = __builtin_amdgcn_raw_buffer_load_b128(
-                    k_rsrc, k_off + 32 * kk * (uint32_t)sizeof(T), soff, K_POLICY);
+            for (int j = 0; j < 4; j++)
+                kd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                    k_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 vd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -244,13 +249,30 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
                 for (int j = 0; j < 4; j++)
                     if (tok0 + 16 * t + 4 * lg + j >= tok_end) va[t][j] = u32x4{0, 0, 0, 0};
         }
+        // K rows through LDS into the A-operand layout: lane (lg, lc) needs row lc, dims
+        // 32kk + 8lg .. +7. One wave per workgroup and LDS operations of a wave complete in
+        // order, so the wave barriers only keep the compiler from moving LDS accesses across.
+        // The second tile's writes follow the first tile's reads in that order.
+        u32x4 kA[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                *reinterpret_cast<u32x4*>(&kt[(4 * lg + j) * DEC_KPITCH + 16 * lc]) = ka[t][j];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                kA[t][kk] = *reinterpret_cast<const u32x4*>(&kt[lc * DEC_KPITCH + 64 * kk + 16 * lg]);
+        }
+        __builtin_amdgcn_wave_barrier();
         // S tiles: s[t][r] = score of head lc for token 16t + 4lg + r of the chunk.
         f32x4 s[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             s[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) s[t] = mfma16x16x32<T>(ka[t][kk], qb[kk], s[t]);
+            for (int kk = 0; kk < 4; kk++) s[t] = mfma16x16x32<T>(kA[t][kk], qb[kk], s[t]);
         }
         float sv[8];
         float tmax = -INFINITY;
@@ -425,44 +447,27 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
 }
 
 // Merge of the pieces of pairs cut by wave ranges, and zero rows for empty contexts: one
-// workgroup per (query head, sequence), one lane per output dim. Pieces are taken 128 at a
-// time (one per lane): their (max, sum) pairs become weights through two block reductions,
+// workgroup per (query head, sequence), one lane per output dim, locating its pieces from the
+// chunk prefix sums the main kernel left in the workspace. Pieces are taken 128 at a time (one
+// per lane): their (max, sum) pairs become weights through two block reductions,
 // then every lane accumulates its dim over the batch with independent loads; batches combine
 // with the same online rescaling as the running update of cpu.rs:96-105.
 template <typename TO>
 __global__ __launch_bounds__(DEC_D) void paged_decode_merge_kernel(
-    TO* __restrict__ out, const int32_t* __restrict__ context_lens, int batch, int num_heads,
-    int kv_heads, int n_rep, int max_ctx, int nwg_i, DecodeWs ws) {
+    TO* __restrict__ out, int batch, int num_heads, int kv_heads, int n_rep, int nwg_i,
+    DecodeWs ws) {
     constexpr int D = DEC_D;
     __shared__ float red_f[DEC_D / 64];
-    __shared__ int red_i[2][DEC_D / 64];
     __shared__ float w_s[DEC_D];
     __shared__ int slot_s[DEC_D];
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x, wv = d >> 6;
-    const int nch = decode_chunks(context_lens[b], max_ctx);
+    // chunks before sequence b, of sequence b and in all sequences (the main kernel's sums)
+    const int before = ws.pre[b], nch = ws.pre[b + 1] - before, all = ws.pre[batch];
     TO* o = out + ((int64_t)b * num_heads + h) * D;
     if (nch == 0) {
         o[d] = from_f32<TO>(0.0f);
         return;
     }
-    // chunks before sequence b, and in all sequences
-    int before = 0, all = 0;
-    for (int i = d; i < batch; i += D) {
-        const int n = decode_chunks(context_lens[i], max_ctx);
-        all += n;
-        if (i < b) before += n;
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        before += __shfl_xor(before, off, 64);
-        all += __shfl_xor(all, off, 64);
-    }
-    if ((d & 63) == 0) {
-        red_i[0][wv] = before;
-        red_i[1][wv] = all;
-    }
-    __syncthreads();
-    before = red_i[0][0] + red_i[0][1];
-    all = red_i[1][0] + red_i[1][1];
     const int g = h / n_rep, hh = h - g * n_rep;
     const int64_t total = (int64_t)kv_heads * all, nwg = nwg_i;
     const int64_t s = (int64_t)kv_heads * before + (int64_t)g * nch;
@@ -473,11 +478,28 @@ __global__ __launch_bounds__(DEC_D) void paged_decode_merge_kernel(
     const int np = (int)(l - f + 1);  // ranges f..l; empty ones wrote nothing
 
     float M = -INFINITY, L = 0.0f, O = 0.0f;
+    const int fslot = (int)(f_first ? 2 * f : 2 * f + 1);  // the first piece always exists
+    // Wave ranges can be empty only when there are fewer chunks than waves; otherwise skip the
+    // (64-bit, slow) range-bound divisions.
+    const bool dense = total >= nwg;
     for (int p0 = 0; p0 < np; p0 += D) {
+        // This lane's dim of the batch's first 8 pieces, loaded before the (max, sum)
+        // reductions, which they do not depend on (a missing piece reads the first piece's
+        // row and gets weight 0).
+        float v0[8];
+        int s0[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int64_t ij = f + p0 + j;
+            s0[j] = (p0 + j < np && (dense || ij * total / nwg != (ij + 1) * total / nwg))
+                        ? (int)((ij == f && !f_first) ? 2 * ij + 1 : 2 * ij)
+                        : -1;
+            v0[j] = ws.o[((int64_t)(s0[j] >= 0 ? s0[j] : fslot) * n_rep + hh) * D + d];
+        }
         const int64_t i = f + p0 + d;
         int slot = -1;
         float mx = -INFINITY, lx = 0.0f;
-        if (p0 + d < np && i * total / nwg != (i + 1) * total / nwg) {
+        if (p0 + d < np && (dense || i * total / nwg != (i + 1) * total / nwg)) {
             slot = (int)((i == f && !f_first) ? 2 * i + 1 : 2 * i);
             mx = ws.ml[2 * ((int64_t)slot * n_rep + hh)];
             lx = ws.ml[2 * ((int64_t)slot * n_rep + hh) + 1];
@@ -498,13 +520,14 @@ __global__ __launch_bounds__(DEC_D) void paged_decode_merge_kernel(
         const float c_old = (M == -INFINITY) ? 0.0f : fast_exp2(M - m_new);
         L = L * c_old + (red_f[0] + red_f[1]);
         O *= c_old;
-        // Unconditional loads (an empty range reads a valid row of the first piece) so they
-        // are all in flight together; the select drops them, so stale workspace bits (even
-        // NaN) never reach the sum.
-        // Groups of 8 straight-line loads: entries past the batch hold slot -1 (weight 0).
+#pragma unroll
+        for (int j = 0; j < 8; j++) O += (s0[j] >= 0) ? w_s[j] * v0[j] : 0.0f;
+        // The rest in groups of 8 unconditional loads (an empty range reads a valid row of the
+        // first piece) so they are all in flight together; the select drops them, so stale
+        // workspace bits (even NaN) never reach the sum. Entries past the batch hold slot -1.
         const int nb8 = (min(D, np - p0) + 7) & ~7;
-        const int sl0 = slot_s[0] >= 0 ? slot_s[0] : slot_s[1];
-        for (int q = 0; q < nb8; q += 8) {
+        const int sl0 = fslot;
+        for (int q = 8; q < nb8; q += 8) {
             float v[8];
             int sl[8];
 #pragma unroll
@@ -537,7 +560,7 @@ static int launch_decode_mfma(void* out, const void* q, const void* k_pool, cons
     int rc = check_hip(hipGetLastError(), "paged_decode launch");
     if (rc != FLOUR_OK) return rc;
     paged_decode_merge_kernel<TO><<<dim3(num_heads, batch), dim3(DEC_D), 0, stream>>>(
-        static_cast<TO*>(out), ctx_lens, batch, num_heads, kv_heads, n_rep, max_ctx, nwg, ws);
+        static_cast<TO*>(out), batch, num_heads, kv_heads, n_rep, nwg, ws);
     return check_hip(hipGetLastError(), "paged_decode merge launch");
 }
 
@@ -560,7 +583,7 @@ extern "C" int flour_hip_paged_decode_workspace_size(int batch, int num_heads, i
         set_error("paged_decode_workspace_size: bad arguments");
         return FLOUR_ERR_INVALID_ARGUMENT;
     }
-    *bytes = decode_ws_bytes(decode_workgroups(), num_heads / kv_heads, head_dim);
+    *bytes = decode_ws_bytes(decode_workgroups(), num_heads / kv_heads, head_dim, batch);
     return FLOUR_OK;
 }
 
@@ -609,7 +632,7 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
                                    s);
     }
     const int nwg = decode_workgroups();
-    const size_t need = decode_ws_bytes(nwg, n_rep, head_dim);
+    const size_t need = decode_ws_bytes(nwg, n_rep, head_dim, batch);
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 256) != 0) {
         set_error("paged_decode: workspace of %zu bytes (256-byte aligned) required, got %zu "
                   "at %p",
@@ -620,6 +643,9 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
     ws.ml = static_cast<float*>(workspace);
     ws.o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                     align256((size_t)2 * nwg * n_rep * 2 * sizeof(float)));
+    ws.pre = reinterpret_cast<int*>(
+        reinterpret_cast<char*>(ws.o) +
+        align256((size_t)2 * nwg * n_rep * (size_t)head_dim * sizeof(float)));
 #define FLOUR_DEC(T)                                                                            \
     do {                                                                                        \
         if (out_dtype == FLOUR_DTYPE_F32)                                                       \

@@ -375,6 +375,18 @@ class KvBatch:
                                         q.ctypes.data_as(ctypes.c_void_p), int(ids.size),
                                         _stream() if self.device_pool else None))
 
+    def step(self, seq_ids, seq_q) -> None:
+        """allocate_kv(seq_ids[i], seq_q[i]) for every sequence, then plan(), in one call; a
+        refused step changes no sequence."""
+        from .ops import _stream
+
+        ids = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int32))
+        q = np.ascontiguousarray(np.asarray(seq_q, dtype=np.int32))
+        assert ids.size == q.size
+        check(lib().flour_kv_batch_step(self._h, ids.ctypes.data_as(ctypes.c_void_p),
+                                        q.ctypes.data_as(ctypes.c_void_p), int(ids.size),
+                                        _stream() if self.device_pool else None))
+
     def write_kv(self, layer: int, k, v) -> None:
         """The planned new rows, packed (rows, kv_heads, head_dim) with a unit last stride."""
         from .ops import _ptr, _stream

@@ -195,6 +195,12 @@ int flour_kv_batch_clear_prefix_cache(flour_kv_batch* b);
  * allocated), packed in this order (cu_seqlens). Sequences must be distinct. */
 int flour_kv_batch_plan(flour_kv_batch* b, const int* seq_ids, const int* seq_q, int n_seqs,
                         void* stream);
+/* allocate_kv(seq_ids[i], seq_q[i]) for every listed sequence, then plan: one call per forward
+ * step (a decode step passes seq_q[i] = 1). Every check (live and distinct sequences,
+ * max_seq_len, max_batch_tokens, free blocks, the device pool) runs before any allocation, so
+ * a refused step leaves every sequence as it was. */
+int flour_kv_batch_step(flour_kv_batch* b, const int* seq_ids, const int* seq_q, int n_seqs,
+                        void* stream);
 /* The KV write of the planned new rows: k/v element (t, h, d) of packed row t at
  * t*stride_tok + h*stride_head + d (flour_hip_kv_write). */
 int flour_kv_batch_write_kv(flour_kv_batch* b, int layer, const void* k, const void* v,

@@ -90,3 +90,27 @@ def test_plan_validation():
         batch_small.plan([t], [10])
     with pytest.raises(_lib.FlourError, match="no device pool"):
         b.plan([s0, s1], [10, 5])
+
+
+def test_step_checks_everything_before_allocating():
+    """flour_kv_batch_step = allocate_kv on every listed sequence + plan; each refusal below
+    leaves lengths, tables and the free list unchanged."""
+    b = batch(num_blocks=4, max_seqs=3, max_seq_len=64, tokens=40)
+    s0, s1 = b.add_sequence(), b.add_sequence()
+    b.allocate_kv(s0, 16)          # one full block: its next row needs a new block
+    b.allocate_kv(s1, 20)
+
+    def state():
+        return [b.len(s0), b.len(s1)], [b.blocks(s0), b.blocks(s1)], b.free_blocks()
+
+    before = state()
+    for ids, q, what in [([s0, s0], [1, 1], "listed twice"),
+                         ([s0, 2], [1, 1], "no live sequence 2"),
+                         ([s0, s1], [1, 0], "brings 0 new rows"),
+                         ([s0, s1], [1, 45], "exceeds max_seq_len 64"),
+                         ([s0, s1], [30, 11], "exceed max_batch_tokens 40"),
+                         ([s0, s1], [17, 13], "out of kv blocks"),   # needs 2 + 1 > 1 free
+                         ([s0, s1], [1, 1], "no device pool")]:       # all checks passed
+        with pytest.raises(_lib.FlourError, match=what):
+            b.step(ids, q)
+        assert state() == before, what

@@ -33,9 +33,10 @@ def rows(n, g, scale=1.0):
     return (torch.randn((n, G, D), generator=g) * scale).to(torch.bfloat16).cuda()
 
 
-def step(b, layer, sids, qn, g):
+def step(b, layer, sids, qn, g, plan=True):
     """Plan, write new K/V rows, attend: returns (q, out) packed in plan order."""
-    b.plan(sids, qn)
+    if plan:
+        b.plan(sids, qn)
     T = sum(qn)
     k, v = rows(T, g), rows(T, g)
     b.write_kv(layer, k, v)
@@ -71,10 +72,13 @@ def test_mixed_prefill_then_decode_steps(device):
         q, out = step(b, layer, sids, lens, g)
         check(b, layer, sids, lens, q, out, f"prefill layer {layer}")
     for t in range(3):  # decode steps: one new row per sequence, the paged decode kernel
-        for s in sids:
-            b.allocate_kv(s, 1)
+        if t == 0:       # allocate_kv per sequence, then plan once per layer
+            for s in sids:
+                b.allocate_kv(s, 1)
+        else:            # flour_kv_batch_step: allocation + plan in one call, kept by all layers
+            b.step(sids, [1] * len(sids))
         for layer in range(2):
-            q, out = step(b, layer, sids, [1] * len(sids), g)
+            q, out = step(b, layer, sids, [1] * len(sids), g, plan=t == 0)
             check(b, layer, sids, [1] * len(sids), q, out, f"decode {t} layer {layer}")
 
 
