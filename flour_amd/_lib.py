@@ -99,6 +99,8 @@ SIGNATURES: dict[str, tuple] = {
     "flour_kv_batch_plan": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "flour_kv_batch_step": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "flour_kv_batch_write_kv": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_i64, _vp]),
+    "flour_kv_batch_rope_write_kv": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_int, _vp,
+                                              _vp, _c_i64, _c_i64, _vp, _vp, _c_int, _vp]),
     "flour_kv_batch_attention": (_c_int, [_vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _c_int,
                                           _c_i64, _c_i64, _c_f, _vp]),
     "flour_kv_batch_pool": (_c_int, [_vp, _c_int, _vp, _vp, _vp]),

@@ -43,7 +43,8 @@ struct KvBatchImpl {
     bool device = false;
     std::vector<void*> k_pools, v_pools;
     // plan arrays: [max_seqs x max_blocks] block tables | [max_seqs] kv lengths |
-    // [max_seqs + 1] cu_seqlens | [max_tokens] slot mapping of the new rows
+    // [max_seqs + 1] cu_seqlens | [max_tokens] slot mapping of the new rows |
+    // [max_tokens] positions of the new rows in their sequences (RoPE table rows)
     int32_t* d_plan = nullptr;
     int32_t* h_plan = nullptr;
     hipEvent_t plan_done = nullptr;
@@ -73,15 +74,17 @@ struct KvBatchImpl {
           live(nseq, 0) {}
 
     int64_t plan_ints() const {
-        return (int64_t)max_seqs * max_blocks + max_seqs + max_seqs + 1 + max_tokens;
+        return (int64_t)max_seqs * max_blocks + max_seqs + max_seqs + 1 + 2 * (int64_t)max_tokens;
     }
     int32_t* d_tables() const { return d_plan; }
     int32_t* d_lens() const { return d_plan + (int64_t)max_seqs * max_blocks; }
     int32_t* d_cu() const { return d_lens() + max_seqs; }
     int32_t* d_slots() const { return d_cu() + max_seqs + 1; }
+    int32_t* d_pos() const { return d_slots() + max_tokens; }
     int64_t off_lens() const { return (int64_t)max_seqs * max_blocks; }
     int64_t off_cu() const { return off_lens() + max_seqs; }
     int64_t off_slots() const { return off_cu() + max_seqs + 1; }
+    int64_t off_pos() const { return off_slots() + max_tokens; }
 
     ~KvBatchImpl() {
         if (plan_done) {
@@ -286,6 +289,7 @@ struct KvBatchImpl {
         int32_t* lens = h_plan + off_lens();
         int32_t* cu = h_plan + off_cu();
         int32_t* slots = h_plan + off_slots();
+        int32_t* pos = h_plan + off_pos();
         cu[0] = 0;
         for (int i = 0; i < n; i++) {
             const BlockTable& t = tables[ids[i]];
@@ -295,13 +299,15 @@ struct KvBatchImpl {
             for (int j = (int)b.size(); j < max_blocks; j++) row[j] = 0;
             lens[i] = t.len();
             cu[i + 1] = cu[i] + q[i];
-            for (int p = t.len() - q[i], k = cu[i]; p < t.len(); p++, k++)
+            for (int p = t.len() - q[i], k = cu[i]; p < t.len(); p++, k++) {
                 slots[k] = (int32_t)t.slot(p);
+                pos[k] = p;
+            }
         }
         const struct {
             int64_t off, n;
-        } parts[4] = {{0, (int64_t)n * max_blocks}, {off_lens(), n}, {off_cu(), n + 1},
-                      {off_slots(), total}};
+        } parts[5] = {{0, (int64_t)n * max_blocks}, {off_lens(), n}, {off_cu(), n + 1},
+                      {off_slots(), total}, {off_pos(), total}};
         for (const auto& pr : parts)
             if (check_hip(hipMemcpyAsync(d_plan + pr.off, h_plan + pr.off, pr.n * sizeof(int32_t),
                                          hipMemcpyHostToDevice, s),
@@ -513,6 +519,27 @@ extern "C" int flour_kv_batch_write_kv(flour_kv_batch* b, int layer, const void*
     return flour_hip_kv_write(k, v, stride_tok, stride_head, x.k_pools[layer], x.v_pools[layer],
                               x.d_slots(), x.plan_total, x.kv_heads, x.head_dim, x.num_slots,
                               x.dtype, stream);
+}
+extern "C" int flour_kv_batch_rope_write_kv(flour_kv_batch* b, int layer, void* q_out,
+                                            const void* q, int64_t q_stride_tok,
+                                            int64_t q_stride_head, int num_heads, const void* k,
+                                            const void* v, int64_t kv_stride_tok,
+                                            int64_t kv_stride_head, const void* cos_table,
+                                            const void* sin_table, int max_pos, void* stream) {
+    clear_error();
+    BATCH_NEED(b, "kv_batch: null");
+    KvBatchImpl& x = b->b;
+    if (int rc = x.need_plan(layer)) return rc;
+    BATCH_NEED(num_heads > 0 && num_heads <= x.num_heads && num_heads % x.kv_heads == 0,
+               "kv_batch: %d query heads (built for up to %d, %d kv heads)", num_heads,
+               x.num_heads, x.kv_heads);
+    BATCH_NEED(max_pos >= x.max_seq_len, "kv_batch: RoPE tables of %d rows do not cover max_seq_len %d",
+               max_pos, x.max_seq_len);
+    return flour_hip_rope_kv_write(q_out, q, q_stride_tok, q_stride_head, num_heads, k, v,
+                                   kv_stride_tok, kv_stride_head, x.k_pools[layer],
+                                   x.v_pools[layer], x.d_slots(), x.d_pos(), cos_table, sin_table,
+                                   max_pos, x.plan_total, x.kv_heads, x.head_dim, x.num_slots,
+                                   x.dtype, stream);
 }
 extern "C" int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void* q,
                                         int num_heads, int64_t q_stride_tok, int64_t q_stride_head,

@@ -395,6 +395,25 @@ class KvBatch:
         check(lib().flour_kv_batch_write_kv(self._h, layer, _ptr(k), _ptr(v), k.stride(0),
                                             k.stride(1), _stream()))
 
+    def rope_write_kv(self, layer: int, q, k, v, cos, sin, q_out=None):
+        """RoPE on the planned rows' q and k at their positions in their sequences, rotated k
+        and v into the layer's pools, in one kernel; returns rope(q) (``q_out=q`` rotates in
+        place). q (rows, num_heads, head_dim), k / v (rows, kv_heads, head_dim), tables from
+        ``ops.rope_tables`` covering max_seq_len positions."""
+        import torch
+        from .ops import _ptr, _stream
+
+        assert k.stride() == v.stride() and k.stride(2) == 1 and q.stride(2) == 1
+        assert q.dtype == k.dtype == v.dtype == cos.dtype == sin.dtype == self.dtype
+        if q_out is None:
+            q_out = torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=q.device)
+        assert q_out.shape == q.shape and q_out.stride() == q.stride()
+        check(lib().flour_kv_batch_rope_write_kv(self._h, layer, _ptr(q_out), _ptr(q), q.stride(0),
+                                                 q.stride(1), q.shape[1], _ptr(k), _ptr(v),
+                                                 k.stride(0), k.stride(1), _ptr(cos), _ptr(sin),
+                                                 cos.shape[0], _stream()))
+        return q_out
+
     def attention(self, layer: int, q, scale: float, out=None, out_dtype=None):
         """Attention of the planned rows: q packed (rows, num_heads, head_dim); returns the
         same shape (decode when every sequence brings one row, varlen prefill otherwise)."""

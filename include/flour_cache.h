@@ -205,6 +205,16 @@ int flour_kv_batch_step(flour_kv_batch* b, const int* seq_ids, const int* seq_q,
  * t*stride_tok + h*stride_head + d (flour_hip_kv_write). */
 int flour_kv_batch_write_kv(flour_kv_batch* b, int layer, const void* k, const void* v,
                             int64_t stride_tok, int64_t stride_head, void* stream);
+/* The fused RoPE + KV write of the planned new rows (flour_hip_rope_kv_write with the plan's
+ * slot mapping and positions: row t of sequence s sits at position len(s) - seq_q(s) + t, the
+ * table row the reference's rope_for_cache uses, attention.rs:96-99 then :104). q is rotated
+ * into q_out (q_out == q rotates in place); rotated k and v go to the layer's pools. The
+ * cos / sin tables ((max_pos, head_dim / 2), storage dtype) must cover max_seq_len positions. */
+int flour_kv_batch_rope_write_kv(flour_kv_batch* b, int layer, void* q_out, const void* q,
+                                 int64_t q_stride_tok, int64_t q_stride_head, int num_heads,
+                                 const void* k, const void* v, int64_t kv_stride_tok,
+                                 int64_t kv_stride_head, const void* cos_table,
+                                 const void* sin_table, int max_pos, void* stream);
 /* Attention of the planned rows: paged decode when every sequence brings one row (q and out
  * (n_seqs, num_heads, head_dim) contiguous), varlen prefill otherwise (strided packed rows). */
 int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void* q, int num_heads,

@@ -115,8 +115,9 @@ int flour_hip_rope_kv_write(void* q_out, const void* q, int64_t q_stride_tok,
  *
  * Long contexts are split across workgroups; partial (max, sum, acc) rows and the batch's
  * per-sequence chunk prefix sums go to `workspace` (device memory, 256-byte aligned, no
- * initialisation needed) and a second kernel on the same stream merges them. flour_hip_paged_decode_workspace_size gives the bytes required; calls
- * that share a workspace must not overlap in time.
+ * initialisation needed) and a second kernel on the same stream merges them.
+ * flour_hip_paged_decode_workspace_size gives the bytes required; calls that share a
+ * workspace must not overlap in time.
  * ---------------------------------------------------------------------------------------- */
 int flour_hip_paged_decode_workspace_size(int batch, int num_heads, int kv_heads, int head_dim,
                                           int max_context_len, size_t* bytes);

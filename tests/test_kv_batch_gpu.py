@@ -4,8 +4,9 @@ A step plans the batch once and every layer runs the KV write and attention over
 sequence's output is checked against the oracle's paged_attention (cpu.rs:57-112) over that
 sequence's own block table in the shared pool: a mixed prefill of sequences of different
 lengths, decode steps for all of them (the paged decode kernel), a shared cached prefix matched
-through the common registry with the suffixes prefilled in one call, and sequences removed and
-added between steps. Tolerances as for the kernels: bf16 max-abs <= 2e-3 and rel-L2 <= 1e-3
+through the common registry with the suffixes prefilled in one call, sequences removed and
+added between steps, and the fused RoPE + KV write of a planned step (bit-exact against the
+oracle's rope_kv_write). Tolerances as for the kernels: bf16 max-abs <= 2e-3 and rel-L2 <= 1e-3
 against the fp32 oracle (fp32 output).
 """
 from __future__ import annotations
@@ -16,7 +17,7 @@ import torch
 
 import oracle as O
 from _util import errors, to_np
-from flour_amd import _lib
+from flour_amd import _lib, ops
 from flour_amd.kv_cache import KvBatch
 
 pytestmark = pytest.mark.gpu
@@ -125,3 +126,42 @@ def test_sequences_leave_and_join_between_steps(device):
     b.allocate_kv(sids[0], 1)
     with pytest.raises(_lib.FlourError, match="no current plan"):
         b.write_kv(0, rows(1, g), rows(1, g))
+
+
+def test_rope_write_then_attention(device):
+    """flour_kv_batch_rope_write_kv: RoPE at each planned row's position in its sequence (the
+    reference's rope_for_cache rows, attention.rs:96-99), rotated k and v into the layer's
+    pool (attention.rs:104), q rotated: bit-exact against the oracle's rope_kv_write on the
+    same rows with slots and positions derived on the host from each sequence's blocks; then
+    attention over the rotated rows against paged_attention. A prefill step, then a decode
+    step."""
+    g = torch.Generator(device="cpu").manual_seed(4)
+    b = make(max_seq_len=1024)
+    cos, sin = ops.rope_tables(1024, D, 500000.0, torch.bfloat16, device)
+    sids = [b.add_sequence() for _ in range(3)]
+    for qn in ([70, 1, 33], [1, 1, 1]):
+        b.step(sids, qn)
+        T = sum(qn)
+        q = torch.randn((T, H, D), generator=g).to(torch.bfloat16).cuda()
+        k, v = rows(T, g), rows(T, g)
+        kp0, vp0 = (to_np(t).copy() for t in b.pool(1))
+        pos, slots = [], []
+        for s, n in zip(sids, qn):
+            bl, L = b.blocks(s), b.len(s)
+            for p in range(L - n, L):
+                pos.append(p)
+                slots.append(bl[p // BS] * BS + p % BS)
+        q_ref, _ = O.rope_kv_write(to_np(q), to_np(k), to_np(v), kp0, vp0,
+                                   np.array(slots, np.int32), np.array(pos, np.int32),
+                                   to_np(cos), to_np(sin), bf16=True)
+        q_rot = b.rope_write_kv(1, q, k, v, cos, sin)
+        torch.cuda.synchronize()
+        kp, vp = (to_np(t) for t in b.pool(1))
+        assert np.array_equal(to_np(q_rot), q_ref)
+        assert np.array_equal(kp, kp0) and np.array_equal(vp, vp0)
+        out = b.attention(1, q_rot, SCALE, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        check(b, 1, sids, qn, q_rot, out, f"rope + attention, rows {qn}")
+    with pytest.raises(_lib.FlourError, match="cover"):
+        short_cos, short_sin = ops.rope_tables(512, D, 500000.0, torch.bfloat16, device)
+        b.rope_write_kv(1, q, k, v, short_cos, short_sin)
