@@ -472,9 +472,22 @@ __global__ __launch_bounds__(DEC_D) void paged_decode_merge_kernel(
     const int64_t total = (int64_t)kv_heads * all, nwg = nwg_i;
     const int64_t s = (int64_t)kv_heads * before + (int64_t)g * nch;
     const int64_t e = s + nch;
-    const int64_t f = owner_wg(s, total, nwg), l = owner_wg(e - 1, total, nwg);
+    // Range owners; 32-bit arithmetic whenever chunks x (waves + 1) fits (it bounds every
+    // numerator below), as it does at any practical size: a 64-bit division is a long
+    // instruction sequence here.
+    int64_t f, l;
+    bool f_first;
+    if ((uint64_t)total * (uint64_t)(nwg + 1) <= 0xffffffffull) {
+        const uint32_t t32 = (uint32_t)total, n32 = (uint32_t)nwg;
+        f = ((uint32_t)(s + 1) * n32 + t32 - 1) / t32 - 1;
+        l = ((uint32_t)e * n32 + t32 - 1) / t32 - 1;
+        f_first = ((uint32_t)s == (uint32_t)f * t32 / n32);
+    } else {
+        f = owner_wg(s, total, nwg);
+        l = owner_wg(e - 1, total, nwg);
+        f_first = (s == f * total / nwg);
+    }
     if (f == l) return;  // finished inside one wave range
-    const bool f_first = (s == f * total / nwg);
     const int np = (int)(l - f + 1);  // ranges f..l; empty ones wrote nothing
 
     float M = -INFINITY, L = 0.0f, O = 0.0f;
