@@ -446,26 +446,25 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     }
 }
 
-// Merge of the pieces of pairs cut by wave ranges, and zero rows for empty contexts: one
-// workgroup per (query head, sequence), one lane per output dim, locating its pieces from the
-// chunk prefix sums the main kernel left in the workspace. Pieces are taken 128 at a time (one
-// per lane): their (max, sum) pairs become weights through two block reductions,
-// then every lane accumulates its dim over the batch with independent loads; batches combine
-// with the same online rescaling as the running update of cpu.rs:96-105.
+// Merge of the pieces of pairs cut by wave ranges, and zero rows for empty contexts: one wave
+// per (query head, sequence), lane i owning output dims 2i and 2i + 1, locating its pieces from
+// the chunk prefix sums the main kernel left in the workspace. Pieces are taken 64 at a time
+// (one per lane): their (max, sum) pairs become weights through wave reductions, then every
+// lane accumulates its two dims over the batch with independent loads, reading each piece's
+// weight and slot from the lane that holds it; batches combine with the same online rescaling
+// as the running update of cpu.rs:96-105. No LDS and no barrier.
 template <typename TO>
-__global__ __launch_bounds__(DEC_D) void paged_decode_merge_kernel(
+__global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     TO* __restrict__ out, int batch, int num_heads, int kv_heads, int n_rep, int nwg_i,
     DecodeWs ws) {
     constexpr int D = DEC_D;
-    __shared__ float red_f[DEC_D / 64];
-    __shared__ float w_s[DEC_D];
-    __shared__ int slot_s[DEC_D];
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x, wv = d >> 6;
+    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     // chunks before sequence b, of sequence b and in all sequences (the main kernel's sums)
     const int before = ws.pre[b], nch = ws.pre[b + 1] - before, all = ws.pre[batch];
-    TO* o = out + ((int64_t)b * num_heads + h) * D;
+    TO* o = out + ((int64_t)b * num_heads + h) * D + 2 * lane;
     if (nch == 0) {
-        o[d] = from_f32<TO>(0.0f);
+        o[0] = from_f32<TO>(0.0f);
+        o[1] = from_f32<TO>(0.0f);
         return;
     }
     const int g = h / n_rep, hh = h - g * n_rep;
@@ -490,71 +489,78 @@ __global__ __launch_bounds__(DEC_D) void paged_decode_merge_kernel(
     if (f == l) return;  // finished inside one wave range
     const int np = (int)(l - f + 1);  // ranges f..l; empty ones wrote nothing
 
-    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    float M = -INFINITY, L = 0.0f, O0 = 0.0f, O1 = 0.0f;
     const int fslot = (int)(f_first ? 2 * f : 2 * f + 1);  // the first piece always exists
     // Wave ranges can be empty only when there are fewer chunks than waves; otherwise skip the
     // (64-bit, slow) range-bound divisions.
     const bool dense = total >= nwg;
-    for (int p0 = 0; p0 < np; p0 += D) {
-        // This lane's dim of the batch's first 8 pieces, loaded before the (max, sum)
-        // reductions, which they do not depend on (a missing piece reads the first piece's
-        // row and gets weight 0).
-        float v0[8];
+    auto piece_slot = [&](int64_t p) -> int {  // slot of piece p (< np), -1 for an empty range
+        const int64_t ij = f + p;
+        if (!dense && ij * total / nwg == (ij + 1) * total / nwg) return -1;
+        return (int)((ij == f && !f_first) ? 2 * ij + 1 : 2 * ij);
+    };
+    auto row = [&](int slot) -> f32x2 {  // this lane's two dims of a piece's partial row
+        return *reinterpret_cast<const f32x2*>(ws.o + ((int64_t)slot * n_rep + hh) * D + 2 * lane);
+    };
+    for (int p0 = 0; p0 < np; p0 += 64) {
+        // The batch's first 8 pieces' rows are loaded before the (max, sum) reductions, which
+        // they do not depend on (a missing piece reads the first piece's row, weight 0).
+        f32x2 v0[8];
         int s0[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int64_t ij = f + p0 + j;
-            s0[j] = (p0 + j < np && (dense || ij * total / nwg != (ij + 1) * total / nwg))
-                        ? (int)((ij == f && !f_first) ? 2 * ij + 1 : 2 * ij)
-                        : -1;
-            v0[j] = ws.o[((int64_t)(s0[j] >= 0 ? s0[j] : fslot) * n_rep + hh) * D + d];
+            s0[j] = p0 + j < np ? piece_slot(p0 + j) : -1;
+            v0[j] = row(s0[j] >= 0 ? s0[j] : fslot);
         }
-        const int64_t i = f + p0 + d;
-        int slot = -1;
+        const int slot = p0 + lane < np ? piece_slot(p0 + lane) : -1;
         float mx = -INFINITY, lx = 0.0f;
-        if (p0 + d < np && (dense || i * total / nwg != (i + 1) * total / nwg)) {
-            slot = (int)((i == f && !f_first) ? 2 * i + 1 : 2 * i);
+        if (slot >= 0) {
             mx = ws.ml[2 * ((int64_t)slot * n_rep + hh)];
             lx = ws.ml[2 * ((int64_t)slot * n_rep + hh) + 1];
         }
         float bm = mx;
         for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
-        if ((d & 63) == 0) red_f[wv] = bm;
-        __syncthreads();
-        const float m_new = fmaxf(M, fmaxf(red_f[0], red_f[1]));
+        const float m_new = fmaxf(M, bm);
         const float w = (slot >= 0) ? fast_exp2(mx - m_new) : 0.0f;
-        w_s[d] = w;
-        slot_s[d] = slot;
         float bl = w * lx;
         for (int off = 32; off > 0; off >>= 1) bl += __shfl_xor(bl, off, 64);
-        __syncthreads();  // red_f reads done; w_s / slot_s visible
-        if ((d & 63) == 0) red_f[wv] = bl;
-        __syncthreads();
         const float c_old = (M == -INFINITY) ? 0.0f : fast_exp2(M - m_new);
-        L = L * c_old + (red_f[0] + red_f[1]);
-        O *= c_old;
+        L = L * c_old + bl;
+        O0 *= c_old;
+        O1 *= c_old;
 #pragma unroll
-        for (int j = 0; j < 8; j++) O += (s0[j] >= 0) ? w_s[j] * v0[j] : 0.0f;
-        // The rest in groups of 8 unconditional loads (an empty range reads a valid row of the
-        // first piece) so they are all in flight together; the select drops them, so stale
-        // workspace bits (even NaN) never reach the sum. Entries past the batch hold slot -1.
-        const int nb8 = (min(D, np - p0) + 7) & ~7;
-        const int sl0 = fslot;
-        for (int q = 8; q < nb8; q += 8) {
-            float v[8];
+        for (int j = 0; j < 8; j++) {
+            const float wj = __shfl(w, j, 64);
+            if (s0[j] >= 0) {
+                O0 += wj * v0[j][0];
+                O1 += wj * v0[j][1];
+            }
+        }
+        // The rest in groups of 8 unconditional loads (a missing piece reads the first piece's
+        // row) so they are all in flight together; the select drops them, so stale workspace
+        // bits (even NaN) never reach the sum.
+        const int nb = min(64, np - p0);
+        for (int q = 8; q < nb; q += 8) {
+            f32x2 v[8];
             int sl[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                sl[j] = slot_s[q + j];
-                v[j] = ws.o[((int64_t)(sl[j] >= 0 ? sl[j] : sl0) * n_rep + hh) * D + d];
+                sl[j] = __shfl(slot, q + j, 64);
+                v[j] = row(sl[j] >= 0 ? sl[j] : fslot);
             }
 #pragma unroll
-            for (int j = 0; j < 8; j++) O += (sl[j] >= 0) ? w_s[q + j] * v[j] : 0.0f;
+            for (int j = 0; j < 8; j++) {
+                const float wj = __shfl(w, q + j, 64);
+                if (sl[j] >= 0) {
+                    O0 += wj * v[j][0];
+                    O1 += wj * v[j][1];
+                }
+            }
         }
         M = m_new;
-        __syncthreads();  // w_s / slot_s / red_f are rewritten by the next batch
     }
-    o[d] = from_f32<TO>(O / L);
+    o[0] = from_f32<TO>(O0 / L);
+    o[1] = from_f32<TO>(O1 / L);
 }
 
 template <typename T, typename TO>
@@ -572,7 +578,7 @@ static int launch_decode_mfma(void* out, const void* q, const void* k_pool, cons
         block_size, num_slots, max_ctx, scale * LOG2E, ws);
     int rc = check_hip(hipGetLastError(), "paged_decode launch");
     if (rc != FLOUR_OK) return rc;
-    paged_decode_merge_kernel<TO><<<dim3(num_heads, batch), dim3(DEC_D), 0, stream>>>(
+    paged_decode_merge_kernel<TO><<<dim3(num_heads, batch), dim3(64), 0, stream>>>(
         static_cast<TO*>(out), batch, num_heads, kv_heads, n_rep, nwg, ws);
     return check_hip(hipGetLastError(), "paged_decode merge launch");
 }
