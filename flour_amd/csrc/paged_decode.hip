@@ -193,28 +193,36 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // cb + i/2, half i%2), so the loop fetches it with v_readlane. Tiles past the segment are
     // clamped to its last tile: every address stays valid, their tokens are masked and their V
     // zeroed in compute_chunk.
-    auto seg_slots = [&](const Seg& sg) -> int {
+    // The block id is kept as loaded and clamped only where a tile load reads it (one segment
+    // later for the next segment): using it here would make the wave wait for this load, and
+    // with it for every chunk load in flight.
+    struct Slots {
+        int id, off;  // lane i: block id and in-block offset of tile i's first token
+    };
+    const int max_id = (int)max_phys;
+    auto seg_slots = [&](const Seg& sg) -> Slots {
         const int32_t* bt = block_tables + (int64_t)sg.b * max_blocks;
         const int last_tile_tok0 = ((sg.tok_end - 1) >> 4) << 4;
         const int tok0 = min(sg.cb * DEC_CHUNK + lane * 16, last_tile_tok0);
         const int lb = BS16 ? (tok0 >> 4) : tok0 / block_size;
-        int64_t phys = bt[lb];  // clamped: a bad block id never leaves the pool
-        phys = phys < 0 ? 0 : (phys > max_phys ? max_phys : phys);
-        return (int)(phys * block_size + (tok0 - lb * block_size));
+        return Slots{bt[lb], tok0 - lb * block_size};
     };
     // Chunk loads as buffer loads: one resource per pool (the kv head's region), the
     // loop-invariant lane offset (VGPR) and the tile's byte offset (SGPR), so there is no
     // per-lane address arithmetic in the loop; non-temporal (K/V are read exactly once);
     // an out-of-region offset reads zeros instead of faulting.
-    auto load_chunk = [&](int g, int slots, int tile0, u32x4 (*kd)[4], u32x4 (*vd)[4]) {
+    auto load_chunk = [&](int g, Slots sl, int tile0, u32x4 (*kd)[4], u32x4 (*vd)[4]) {
         const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(k_pool + (int64_t)g * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
         const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(v_pool + (int64_t)g * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
 #pragma unroll
         for (int t = 0; t < 2; t++) {
+            int id = __builtin_amdgcn_readlane(sl.id, tile0 + t);
+            id = id < 0 ? 0 : (id > max_id ? max_id : id);  // a bad block id never leaves the pool
             const uint32_t soff =
-                (uint32_t)__builtin_amdgcn_readlane(slots, tile0 + t) * (uint32_t)(D * sizeof(T));
+                (uint32_t)(id * block_size + __builtin_amdgcn_readlane(sl.off, tile0 + t)) *
+                (uint32_t)(D * sizeof(T));
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 kd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -378,11 +386,11 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // wait counts stay exact) are in flight while the current chunk is computed and while a
     // finished piece is written out.
     Seg cur = seg_at(lo);
-    int cur_slots = seg_slots(cur);
+    Slots cur_slots = seg_slots(cur);
     int64_t nx = lo + (cur.ce - cur.cb);
     bool has_nxt = nx < hi;
     Seg nxt = cur;
-    int nxt_slots = cur_slots;
+    Slots nxt_slots = cur_slots;
     if (has_nxt) {
         nxt = seg_at(nx);
         nxt_slots = seg_slots(nxt);
@@ -397,15 +405,31 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // from (kc, vc), then advance the cursor.
     auto step = [&](auto prefetch, u32x4 (*kc)[4], u32x4 (*vc)[4], u32x4 (*kn)[4],
                     u32x4 (*vn)[4]) {
+        const bool seg_end = c + 1 >= cur.ce;
+        // At a segment's last chunk the segment after the next one is looked up and its
+        // block-table entries are requested before this step's chunk loads, so the rotation at
+        // the end of the step waits for that load alone and not for the chunk loads behind it.
+        int64_t nn_x = nx;
+        bool has_nn = false;
+        Seg nn = nxt;
+        Slots nn_slots = nxt_slots;
+        if (seg_end && has_nxt) {
+            nn_x = nx + (nxt.ce - nxt.cb);
+            has_nn = nn_x < hi;
+            if (has_nn) {
+                nn = seg_at(nn_x);
+                nn_slots = seg_slots(nn);
+            }
+        }
         if constexpr (decltype(prefetch)::value) {
             const bool in_cur = c + 1 < cur.ce;
             const int pg = in_cur ? cur.g : nxt.g;
-            const int pslots = in_cur ? cur_slots : nxt_slots;
+            const Slots pslots = in_cur ? cur_slots : nxt_slots;
             const int ptile = in_cur ? 2 * (c + 1 - cur.cb) : 0;
             load_chunk(pg, pslots, ptile, kn, vn);
         }
         compute_chunk(c, cur.tok_end, kc, vc);
-        if (c + 1 < cur.ce) {
+        if (!seg_end) {
             c += 1;
             return;
         }
@@ -421,11 +445,11 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
         cur = nxt;
         cur_slots = nxt_slots;
         c = cur.cb;
-        nx += cur.ce - cur.cb;
-        has_nxt = nx < hi;
-        if (has_nxt) {
-            nxt = seg_at(nx);
-            nxt_slots = seg_slots(nxt);
+        nx = nn_x;
+        has_nxt = has_nn;
+        if (has_nn) {
+            nxt = nn;
+            nxt_slots = nn_slots;
         }
     };
 
