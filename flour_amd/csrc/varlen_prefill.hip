@@ -322,7 +322,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // with vector loads. Scalar loads would share the LDS wait counter, so every LDS wait of a
     // tile would also wait for them.
     uint32_t win_cur = 0, win_next = 0, win_pre = 0;  // win_pre: first window of the next item
+    uint32_t win_ld = 0;  // entries wbase + 128 + i once ld_ok: becomes win_next at the crossing
     int wbase = 0;
+    bool ld_ok = false;
     auto load_window = [&](const int32_t* row, int base, int n_entries) __attribute__((always_inline)) {
         const int e = min(base + lane, n_entries - 1);  // entries past the last page are unused
         return (uint32_t)row[e];
@@ -332,11 +334,21 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // the last page (their loads are masked off). Tiles are visited in non-decreasing order.
     auto page_bases = [&](int kt, int* pb) {
         const int lb0 = min(BS16 ? (kt * PF_KT) >> 4 : kt * PF_KT / block_size, last_page);
-        while (lb0 - wbase >= 64) {
+        // lb0 grows by at most PF_KT / block_size <= 4 pages a call (block_size is a multiple of
+        // 16), so a call crosses at most one window, and the call before a crossing already
+        // had lb0 + 4 - wbase >= 64 and issued the refill into win_ld. The crossing then only
+        // moves values loaded at least one tile load earlier: a register move of a value that
+        // is still the newest load in flight would wait for every tile load behind it.
+        if (lb0 - wbase >= 64) {
             asm volatile("" ::: "memory");
             win_cur = win_next;
+            win_next = win_ld;
             wbase += 64;
-            win_next = load_window(bt, wbase + 64, last_page + 1);
+            ld_ok = false;
+        }
+        if (!ld_ok && lb0 + 4 - wbase >= 64) {
+            win_ld = load_window(bt, wbase + 128, last_page + 1);
+            ld_ok = true;
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -604,6 +616,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         load_q(it);
         win_cur = win_pre;
         wbase = 0;
+        ld_ok = false;
         win_next = load_window(bt, 64, last_page + 1);
         if (after.valid)  // first window of the item after this one
             win_pre = load_window(block_tables + (int64_t)after.seq * max_blocks, 0,
