@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <exception>
+#include <new>
 #include <string>
 
 #include "flour_hip.h"
@@ -192,8 +194,28 @@ __device__ __forceinline__ float sum_across_rows(float x) {
 }
 
 // ------------------------------------------------------------------ host-side error state
-void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
-void clear_error();
+// Both are noexcept: the message lives in a fixed per-thread buffer.
+void set_error(const char* fmt, ...) noexcept __attribute__((format(printf, 1, 2)));
+void clear_error() noexcept;
+
+// Runs the body of a C entry point so that no C++ exception crosses the C ABI (the caller may
+// be C, ctypes or another language's FFI): a failed host allocation in a container or `new`
+// becomes FLOUR_ERR_CAPACITY with a message, any other exception FLOUR_ERR_INVALID_ARGUMENT.
+template <typename F>
+int abi_guard(const char* what, F&& body) noexcept {
+    try {
+        return body();
+    } catch (const std::bad_alloc&) {
+        set_error("%s: out of host memory", what);
+        return FLOUR_ERR_CAPACITY;
+    } catch (const std::exception& e) {
+        set_error("%s: %s", what, e.what());
+        return FLOUR_ERR_INVALID_ARGUMENT;
+    } catch (...) {
+        set_error("%s: unexpected exception", what);
+        return FLOUR_ERR_INVALID_ARGUMENT;
+    }
+}
 
 inline int elem_bytes(int dtype) { return dtype == FLOUR_DTYPE_F32 ? 4 : 2; }
 inline bool valid_dtype(int dtype) {

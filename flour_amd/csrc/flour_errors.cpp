@@ -2,24 +2,22 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <string>
-
 #include "flour_common.h"
 
 namespace flour {
 
-static thread_local std::string g_last_error;
+// A fixed buffer, so that recording an error never allocates (it may report a failed
+// allocation); longer messages are truncated.
+static thread_local char g_last_error[512];
 
-void set_error(const char* fmt, ...) {
-    char buf[512];
+void set_error(const char* fmt, ...) noexcept {
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof(buf), fmt, ap);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
     va_end(ap);
-    g_last_error = buf;
 }
 
-void clear_error() { g_last_error.clear(); }
+void clear_error() noexcept { g_last_error[0] = '\0'; }
 
 int check_hip(hipError_t e, const char* what) {
     if (e == hipSuccess) return FLOUR_OK;
@@ -29,6 +27,6 @@ int check_hip(hipError_t e, const char* what) {
 
 }  // namespace flour
 
-extern "C" const char* flour_hip_last_error(void) { return flour::g_last_error.c_str(); }
+extern "C" const char* flour_hip_last_error(void) { return flour::g_last_error; }
 
 extern "C" const char* flour_hip_version(void) { return "flour_hip 0.1.0 (gfx950)"; }

@@ -20,6 +20,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <memory>
 #include <vector>
 
 #include "flour_cache.h"
@@ -67,7 +68,7 @@ struct KvBatchImpl {
           block_size(bs),
           dtype(dt),
           num_blocks(nblk),
-          max_blocks((max_len + bs - 1) / bs),
+          max_blocks((int)(((int64_t)max_len + bs - 1) / bs)),
           num_slots((int64_t)nblk * bs),
           allocator(nblk),
           tables(nseq, BlockTable(bs)),
@@ -178,6 +179,7 @@ struct KvBatchImpl {
                       (long long)end, max_seq_len);
             return FLOUR_ERR_CAPACITY;
         }
+        t.reserve_blocks((end + block_size - 1) / block_size);
         while (t.capacity() < end) {
             const int b = allocator.allocate();
             if (b < 0) {
@@ -202,13 +204,14 @@ struct KvBatchImpl {
         const int reusable = (n % bs == 0) ? (full > 0 ? full - 1 : 0) : full;
         uint64_t parent = PREFIX_SEED;
         int matched = 0;
+        t.reserve_blocks(reusable);
         for (int b = 0; b < reusable; b++) {
             const uint32_t* chunk = tok + (int64_t)b * bs;
             const uint64_t h = block_hash(parent, chunk, bs);
             const int blk = registry.get(h, chunk, bs);
             if (blk < 0) break;
-            allocator.incref(blk);
             t.push_block(blk);
+            allocator.incref(blk);
             matched += bs;
             parent = h;
         }
@@ -232,8 +235,8 @@ struct KvBatchImpl {
             const uint64_t h = block_hash(parent, chunk, bs);
             if (!registry.contains(h)) {
                 const int blk = t.block_at(b);
-                allocator.incref(blk);
                 registry.insert(h, chunk, bs, blk);
+                allocator.incref(blk);
             }
             parent = h;
         }
@@ -368,6 +371,11 @@ struct KvBatchImpl {
             set_error("kv_batch: no device pool");
             return FLOUR_ERR_UNSUPPORTED;
         }
+        // table room first (the only step that can fail now), so no sequence changes unless all do
+        for (int i = 0; i < n; i++) {
+            BlockTable& t = tables[ids[i]];
+            t.reserve_blocks((t.len() + (int64_t)q[i] + block_size - 1) / block_size);
+        }
         for (int i = 0; i < n; i++)
             if (int rc = allocate_kv(ids[i], q[i])) return rc;  // cannot fail after the checks
         return plan(ids, q, n, s);
@@ -420,18 +428,17 @@ extern "C" int flour_kv_batch_create(int num_layers, int num_blocks, int max_seq
                kv_heads, head_dim, block_size, dtype);
     BATCH_NEED((int64_t)num_blocks * block_size < (1ll << 31),
                "kv_batch: %lld slots exceed int32 slot ids", (long long)num_blocks * block_size);
-    auto* x = new flour_kv_batch{KvBatchImpl(num_layers, num_blocks, max_seqs, max_seq_len,
-                                             max_batch_tokens, num_heads, kv_heads, head_dim,
-                                             block_size, dtype)};
-    if (device_pool) {
-        const int rc = x->b.alloc_device();
-        if (rc != FLOUR_OK) {
-            delete x;
-            return rc;
+    return abi_guard("kv_batch", [&]() -> int {
+        std::unique_ptr<flour_kv_batch> x(new flour_kv_batch{
+            KvBatchImpl(num_layers, num_blocks, max_seqs, max_seq_len, max_batch_tokens, num_heads,
+                        kv_heads, head_dim, block_size, dtype)});
+        if (device_pool) {
+            const int rc = x->b.alloc_device();
+            if (rc != FLOUR_OK) return rc;
         }
-    }
-    *out = x;
-    return FLOUR_OK;
+        *out = x.release();
+        return FLOUR_OK;
+    });
 }
 extern "C" void flour_kv_batch_destroy(flour_kv_batch* b) { delete b; }
 
@@ -453,7 +460,7 @@ extern "C" int flour_kv_batch_reset_sequence(flour_kv_batch* b, int seq_id) {
 extern "C" int flour_kv_batch_allocate_kv(flour_kv_batch* b, int seq_id, int seq_len) {
     clear_error();
     BATCH_NEED(b, "kv_batch: null");
-    return b->b.allocate_kv(seq_id, seq_len);
+    return abi_guard("kv_batch", [&] { return b->b.allocate_kv(seq_id, seq_len); });
 }
 extern "C" int flour_kv_batch_len(const flour_kv_batch* b, int seq_id) {
     clear_error();
@@ -473,7 +480,7 @@ extern "C" int flour_kv_batch_ref_count(const flour_kv_batch* b, int block_id) {
 extern "C" int flour_kv_batch_blocks(const flour_kv_batch* b, int seq_id, int32_t* out, int cap,
                                      int* n) {
     clear_error();
-    BATCH_NEED(b && n, "kv_batch: bad arguments");
+    BATCH_NEED(b && n && (out || cap == 0), "kv_batch: bad arguments");
     if (int rc = b->b.need_live(seq_id)) return rc;
     const auto& v = b->b.tables[seq_id].blocks();
     *n = (int)v.size();
@@ -484,31 +491,37 @@ extern "C" int flour_kv_batch_match_prefix(flour_kv_batch* b, int seq_id, const 
                                            int n) {
     clear_error();
     BATCH_NEED(b && (tokens || n == 0) && n >= 0, "kv_batch: bad arguments");
-    return b->b.match_prefix(seq_id, tokens, n);
+    return abi_guard("kv_batch", [&] { return b->b.match_prefix(seq_id, tokens, n); });
 }
 extern "C" int flour_kv_batch_register_prefix(flour_kv_batch* b, int seq_id,
                                               const uint32_t* tokens, int n) {
     clear_error();
     BATCH_NEED(b && (tokens || n == 0) && n >= 0, "kv_batch: bad arguments");
-    return b->b.register_prefix(seq_id, tokens, n);
+    return abi_guard("kv_batch", [&] { return b->b.register_prefix(seq_id, tokens, n); });
 }
 extern "C" int flour_kv_batch_clear_prefix_cache(flour_kv_batch* b) {
     clear_error();
     BATCH_NEED(b, "kv_batch: null");
-    b->b.clear_prefix_cache();
-    return FLOUR_OK;
+    return abi_guard("kv_batch", [&]() -> int {
+        b->b.clear_prefix_cache();
+        return FLOUR_OK;
+    });
 }
 extern "C" int flour_kv_batch_plan(flour_kv_batch* b, const int* seq_ids, const int* seq_q,
                                    int n_seqs, void* stream) {
     clear_error();
     BATCH_NEED(b, "kv_batch: null");
-    return b->b.plan(seq_ids, seq_q, n_seqs, static_cast<hipStream_t>(stream));
+    return abi_guard("kv_batch", [&] {
+        return b->b.plan(seq_ids, seq_q, n_seqs, static_cast<hipStream_t>(stream));
+    });
 }
 extern "C" int flour_kv_batch_step(flour_kv_batch* b, const int* seq_ids, const int* seq_q,
                                    int n_seqs, void* stream) {
     clear_error();
     BATCH_NEED(b, "kv_batch: null");
-    return b->b.step(seq_ids, seq_q, n_seqs, static_cast<hipStream_t>(stream));
+    return abi_guard("kv_batch", [&] {
+        return b->b.step(seq_ids, seq_q, n_seqs, static_cast<hipStream_t>(stream));
+    });
 }
 extern "C" int flour_kv_batch_write_kv(flour_kv_batch* b, int layer, const void* k, const void* v,
                                        int64_t stride_tok, int64_t stride_head, void* stream) {

@@ -18,6 +18,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <memory>
 #include <unordered_map>
 #include <vector>
 
@@ -64,12 +65,12 @@ struct KvCacheImpl {
           head_dim(D),
           block_size(bs),
           dtype(dt),
-          num_blocks((max_len + bs - 1) / bs),
-          num_slots((int64_t)((max_len + bs - 1) / bs) * bs),
-          allocator((max_len + bs - 1) / bs),
+          num_blocks((int)(((int64_t)max_len + bs - 1) / bs)),
+          num_slots((int64_t)num_blocks * bs),
+          allocator(num_blocks),
           table(bs) {}
 
-    int meta_ints() const { return num_blocks + 3 + max_seq_len; }
+    int64_t meta_ints() const { return (int64_t)num_blocks + 3 + max_seq_len; }
     int32_t* d_table() const { return d_meta; }
     int32_t* d_kv_len() const { return d_meta + num_blocks; }
     int32_t* d_cu() const { return d_meta + num_blocks + 1; }
@@ -176,6 +177,7 @@ struct KvCacheImpl {
                       (long long)end, max_seq_len);
             return FLOUR_ERR_CAPACITY;
         }
+        table.reserve_blocks((end + table.block_size() - 1) / table.block_size());
         while (table.capacity() < end) {
             const int id = allocator.allocate();
             if (id < 0) {
@@ -201,13 +203,14 @@ struct KvCacheImpl {
         const int reusable = (n % bs == 0) ? (full > 0 ? full - 1 : 0) : full;
         uint64_t parent = PREFIX_SEED;
         int matched = 0;
+        table.reserve_blocks(reusable);
         for (int b = 0; b < reusable; b++) {
             const uint32_t* chunk = tok + (int64_t)b * bs;
             const uint64_t h = block_hash(parent, chunk, bs);
             const int id = registry.get(h, chunk, bs);
             if (id < 0) break;
-            allocator.incref(id);
             table.push_block(id);
+            allocator.incref(id);
             table_version++;
             matched += bs;
             parent = h;
@@ -230,8 +233,8 @@ struct KvCacheImpl {
             const uint64_t h = block_hash(parent, chunk, bs);
             if (!registry.contains(h)) {
                 const int id = table.block_at(b);
-                allocator.incref(id);  // the registry holds its own reference
                 registry.insert(h, chunk, bs, id);
+                allocator.incref(id);  // the registry holds its own reference
             }
             parent = h;
         }
@@ -424,6 +427,7 @@ struct KvCacheImpl {
         }
         std::vector<int> allocated;
         allocated.reserve(nb);
+        table.reserve_blocks(nb);
         auto roll_back = [&](int rc) {
             for (int id : allocated) allocator.decref(id);
             table.clear();
@@ -465,8 +469,8 @@ struct KvCacheImpl {
             const uint64_t h = block_hash(parent, chunk, bs);
             if (!registry.contains(h)) {
                 const int id = table.block_at(b);
-                allocator.incref(id);
                 registry.insert(h, chunk, bs, id);
+                allocator.incref(id);
             }
             parent = h;
         }
@@ -503,8 +507,10 @@ struct flour_kv_cache {
 extern "C" int flour_block_allocator_create(int num_blocks, flour_block_allocator** out) {
     clear_error();
     FLOUR_NEED(out && num_blocks >= 0, "block_allocator: bad arguments");
-    *out = new flour_block_allocator{BlockAllocator(num_blocks)};
-    return FLOUR_OK;
+    return abi_guard("block_allocator", [&]() -> int {
+        *out = new flour_block_allocator{BlockAllocator(num_blocks)};
+        return FLOUR_OK;
+    });
 }
 extern "C" void flour_block_allocator_destroy(flour_block_allocator* a) { delete a; }
 extern "C" int flour_block_allocator_allocate(flour_block_allocator* a) {
@@ -539,15 +545,19 @@ extern "C" int flour_block_allocator_num_free(const flour_block_allocator* a) {
 extern "C" int flour_block_table_create(int block_size, flour_block_table** out) {
     clear_error();
     FLOUR_NEED(out && block_size > 0, "block_table: bad arguments");
-    *out = new flour_block_table{BlockTable(block_size)};
-    return FLOUR_OK;
+    return abi_guard("block_table", [&]() -> int {
+        *out = new flour_block_table{BlockTable(block_size)};
+        return FLOUR_OK;
+    });
 }
 extern "C" void flour_block_table_destroy(flour_block_table* t) { delete t; }
 extern "C" int flour_block_table_push_block(flour_block_table* t, int id) {
     clear_error();
     FLOUR_NEED(t && id >= 0, "block_table: bad block id %d", id);
-    t->t.push_block(id);
-    return FLOUR_OK;
+    return abi_guard("block_table", [&]() -> int {
+        t->t.push_block(id);
+        return FLOUR_OK;
+    });
 }
 extern "C" int flour_block_table_advance(flour_block_table* t, int n) {
     clear_error();
@@ -604,27 +614,26 @@ extern "C" int flour_kv_cache_create(int num_layers, int max_seq_len, int num_he
                "kv_cache: bad shape (layers=%d max_seq_len=%d heads=%d kv_heads=%d head_dim=%d "
                "block_size=%d dtype=%d)",
                num_layers, max_seq_len, num_heads, kv_heads, head_dim, block_size, dtype);
-    const int64_t slots = (int64_t)((max_seq_len + block_size - 1) / block_size) * block_size;
+    const int64_t slots = ((int64_t)max_seq_len + block_size - 1) / block_size * block_size;
     FLOUR_NEED(slots < (1ll << 31), "kv_cache: %lld slots exceed int32 slot ids",
                (long long)slots);
-    auto* c = new flour_kv_cache{KvCacheImpl(num_layers, max_seq_len, num_heads, kv_heads,
-                                             head_dim, block_size, dtype)};
-    if (device_pool) {
-        const int rc = c->c.alloc_device();
-        if (rc != FLOUR_OK) {
-            delete c;
-            return rc;
+    return abi_guard("kv_cache", [&]() -> int {
+        std::unique_ptr<flour_kv_cache> c(new flour_kv_cache{KvCacheImpl(
+            num_layers, max_seq_len, num_heads, kv_heads, head_dim, block_size, dtype)});
+        if (device_pool) {
+            const int rc = c->c.alloc_device();
+            if (rc != FLOUR_OK) return rc;
         }
-    }
-    *out = c;
-    return FLOUR_OK;
+        *out = c.release();
+        return FLOUR_OK;
+    });
 }
 extern "C" void flour_kv_cache_destroy(flour_kv_cache* c) { delete c; }
 
 extern "C" int flour_kv_cache_allocate_kv(flour_kv_cache* c, int seq_len) {
     clear_error();
     FLOUR_NEED(c, "kv_cache: null");
-    return c->c.allocate_kv(seq_len);
+    return abi_guard("kv_cache", [&] { return c->c.allocate_kv(seq_len); });
 }
 extern "C" int flour_kv_cache_len(const flour_kv_cache* c) { return c ? c->c.table.len() : -1; }
 extern "C" int flour_kv_cache_capacity(const flour_kv_cache* c) {
@@ -734,26 +743,30 @@ extern "C" int flour_kv_cache_match_prefix(flour_kv_cache* c, const uint32_t* to
     FLOUR_NEED(c && n >= 0 && (tokens || n == 0), "kv_cache: bad token list");
     FLOUR_NEED(c->c.table.blocks().empty() && c->c.table.len() == 0,
                "kv_cache: match_prefix needs a freshly reset sequence");
-    return c->c.match_prefix(tokens, n);
+    return abi_guard("kv_cache", [&] { return c->c.match_prefix(tokens, n); });
 }
 extern "C" int flour_kv_cache_register_prefix(flour_kv_cache* c, const uint32_t* tokens, int n) {
     clear_error();
     FLOUR_NEED(c && n >= 0 && (tokens || n == 0), "kv_cache: bad token list");
-    return c->c.register_prefix(tokens, n);
+    return abi_guard("kv_cache", [&] { return c->c.register_prefix(tokens, n); });
 }
 extern "C" int flour_kv_cache_clear_prefix_cache(flour_kv_cache* c) {
     clear_error();
     FLOUR_NEED(c, "kv_cache: null");
-    c->c.clear_prefix_cache();
-    return FLOUR_OK;
+    return abi_guard("kv_cache", [&]() -> int {
+        c->c.clear_prefix_cache();
+        return FLOUR_OK;
+    });
 }
 extern "C" int flour_kv_cache_export_bundle(flour_kv_cache* c, const char* model_id,
                                             const uint32_t* token_ids, int n_ids, int token_count,
                                             void* out, size_t cap, size_t* len, void* stream) {
     clear_error();
     FLOUR_NEED(c && len, "kv_cache: bad arguments");
-    return c->c.export_bundle(model_id, token_ids, n_ids, token_count, out, cap, len,
-                              static_cast<hipStream_t>(stream));
+    return abi_guard("kv bundle export", [&] {
+        return c->c.export_bundle(model_id, token_ids, n_ids, token_count, out, cap, len,
+                                  static_cast<hipStream_t>(stream));
+    });
 }
 extern "C" int flour_kv_cache_import_bundle(flour_kv_cache* c, const void* bytes, size_t len,
                                             const uint32_t* prompt_tokens, int n_prompt,
@@ -761,8 +774,10 @@ extern "C" int flour_kv_cache_import_bundle(flour_kv_cache* c, const void* bytes
     clear_error();
     FLOUR_NEED(c && imported, "kv_cache: bad arguments");
     *imported = 0;
-    return c->c.import_bundle(bytes, len, prompt_tokens, n_prompt, imported,
-                              static_cast<hipStream_t>(stream));
+    return abi_guard("kv bundle import", [&] {
+        return c->c.import_bundle(bytes, len, prompt_tokens, n_prompt, imported,
+                                  static_cast<hipStream_t>(stream));
+    });
 }
 extern "C" int flour_kv_cache_pool(const flour_kv_cache* c, int layer, void** k_pool,
                                    void** v_pool, int64_t* num_slots) {

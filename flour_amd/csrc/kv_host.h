@@ -59,6 +59,9 @@ class BlockTable {
     int block_size() const { return bs_; }
     int capacity() const { return (int)blocks_.size() * bs_; }
     void push_block(int id) { blocks_.push_back(id); }
+    // room for n blocks in all, so that the pushes up to n cannot fail (callers reserve
+    // before they take references, so a failed allocation changes no reference count)
+    void reserve_blocks(int64_t n) { blocks_.reserve((size_t)n); }
     const std::vector<int>& blocks() const { return blocks_; }
     int block_at(int i) const { return blocks_[i]; }
     void clear() {

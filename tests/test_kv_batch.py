@@ -114,3 +114,32 @@ def test_step_checks_everything_before_allocating():
         with pytest.raises(_lib.FlourError, match=what):
             b.step(ids, q)
         assert state() == before, what
+
+
+def test_block_list_query_needs_a_buffer_for_a_positive_capacity():
+    """flour_kv_batch_blocks reports the count with no buffer only when cap is 0; a null buffer
+    with room claimed is refused, not written through."""
+    import ctypes
+
+    b = batch()
+    s = b.add_sequence()
+    b.allocate_kv(s, 20)
+    n = ctypes.c_int(-1)
+    assert _lib.lib().flour_kv_batch_blocks(b._h, s, None, 4, ctypes.byref(n)) == \
+        _lib.ERR_INVALID_ARGUMENT
+    assert _lib.lib().flour_kv_batch_blocks(b._h, s, None, 0, ctypes.byref(n)) == _lib.OK
+    assert n.value == 2
+
+
+def test_error_message_is_cleared_by_the_next_successful_call():
+    """flour_hip_last_error describes the last failing call of this thread; every entry point
+    clears it first, so a success leaves it empty."""
+    b = batch()
+    s = b.add_sequence()
+    b.allocate_kv(s, 32)
+    with pytest.raises(_lib.FlourError, match="register_prefix over 1000 full blocks"):
+        b.register_prefix(s, list(range(16000)))
+    assert _lib.lib().flour_hip_last_error().decode().startswith(
+        "kv_batch: register_prefix over 1000 full blocks")
+    b.allocate_kv(s, 1)
+    assert _lib.lib().flour_hip_last_error().decode() == ""
