@@ -6,12 +6,18 @@
 // `i == slots[i]`; for mappings without such a run start both agree bit for bit, and this
 // kernel implements the scatter for every mapping (the quirk is a reference bug).
 //
-// Design: HBM-bound byte copy. One workgroup moves the rows of a group of tokens; each lane
-// moves one 16-byte (or narrower, when alignment forbids) vector of K and the same of V, so a
-// 128-dim bf16 row (256 B) is 16 lanes and a wave moves 4 full rows per instruction.
+// Design: HBM-bound byte copy. A lane moves one 16-byte (or narrower, when alignment forbids)
+// vector of K and the same of V for each of KW_ROUNDS tokens, so a 128-dim bf16 row (256 B) is
+// 16 lanes and a wave moves 4 full rows per instruction. A lane reads its tokens' slots, then
+// issues every load, then every store: one latency chain (slot, rows) per lane instead of one
+// per token, and a grid small enough to be resident at once.
 #include "flour_common.h"
 
 namespace flour {
+
+// Tokens per lane (a workgroup covers KW_ROUNDS groups). Measured on a 9.6K-token batch:
+// 1 -> 18.8 us, 2 and 4 -> 17.8 us, 8 -> 19.5 us.
+static constexpr int KW_ROUNDS = 4;
 
 template <typename VecT>
 __global__ __launch_bounds__(256) void kv_write_kernel(
@@ -23,21 +29,45 @@ __global__ __launch_bounds__(256) void kv_write_kernel(
     const int t_local = threadIdx.x / per_token;
     const int rem = threadIdx.x - t_local * per_token;
     if (t_local >= tokens_per_block) return;
-    const int64_t t = (int64_t)blockIdx.x * tokens_per_block + t_local;
-    if (t >= num_tokens) return;
-    const int64_t slot = slot_mapping[t];
-    if (slot < 0 || slot >= num_slots) return;  // padding token / never write out of bounds
     const int h = rem / vecs_per_row;
     const int c = rem - h * vecs_per_row;
-    const int64_t src = t * stride_tok_b + (int64_t)h * stride_head_b + (int64_t)c * sizeof(VecT);
-    const int64_t dst = ((int64_t)h * num_slots + slot) * row_bytes + (int64_t)c * sizeof(VecT);
-    const VecT kv = *reinterpret_cast<const VecT*>(k + src);
-    const VecT vv = *reinterpret_cast<const VecT*>(v + src);
-    *reinterpret_cast<VecT*>(k_pool + dst) = kv;
-    *reinterpret_cast<VecT*>(v_pool + dst) = vv;
+    const int64_t src_lane = (int64_t)h * stride_head_b + (int64_t)c * sizeof(VecT);
+    const int64_t dst_lane = (int64_t)h * num_slots * row_bytes + (int64_t)c * sizeof(VecT);
+    // Token of round i: consecutive groups of tokens_per_block tokens. Loads are unconditional
+    // (a token past the end reads the last token's row, a padding token its own row) so that the
+    // compiler issues them back to back; only the stores are guarded.
+    const int64_t t0 = (int64_t)blockIdx.x * tokens_per_block * KW_ROUNDS + t_local;
+    int64_t slot[KW_ROUNDS];
+#pragma unroll
+    for (int i = 0; i < KW_ROUNDS; i++) {
+        const int64_t t = t0 + (int64_t)i * tokens_per_block;
+        slot[i] = slot_mapping[t < num_tokens ? t : num_tokens - 1];
+    }
+    VecT kv[KW_ROUNDS], vv[KW_ROUNDS];
+#pragma unroll
+    for (int i = 0; i < KW_ROUNDS; i++) {
+        const int64_t t = t0 + (int64_t)i * tokens_per_block;
+        const int64_t src = (t < num_tokens ? t : num_tokens - 1) * stride_tok_b + src_lane;
+        kv[i] = *reinterpret_cast<const VecT*>(k + src);
+        vv[i] = *reinterpret_cast<const VecT*>(v + src);
+    }
+    // keep the loads here (slots and rows): otherwise the compiler sinks each into its guarded
+    // store, where it becomes a conditional load that is waited for before the next is issued
+#pragma unroll
+    for (int i = 0; i < KW_ROUNDS; i++) asm volatile("" ::"v"(kv[i]), "v"(vv[i]), "v"(slot[i]));
+#pragma unroll
+    for (int i = 0; i < KW_ROUNDS; i++) {
+        const int64_t t = t0 + (int64_t)i * tokens_per_block;
+        // tokens past the end, padding tokens (slot < 0) and slots outside the pool are skipped
+        if (t < num_tokens && slot[i] >= 0 && slot[i] < num_slots) {
+            const int64_t dst = slot[i] * row_bytes + dst_lane;
+            *reinterpret_cast<VecT*>(k_pool + dst) = kv[i];
+            *reinterpret_cast<VecT*>(v_pool + dst) = vv[i];
+        }
+    }
 }
 
-// Per-token workgroup shape: enough whole tokens to fill up to 256 lanes.
+// Workgroup shape: enough whole tokens to fill up to 256 lanes, KW_ROUNDS groups of them.
 template <typename VecT>
 static int launch_kv_write(const void* k, const void* v, int64_t stride_tok, int64_t stride_head,
                            void* k_pool, void* v_pool, const int32_t* slots, int num_tokens,
@@ -53,7 +83,8 @@ static int launch_kv_write(const void* k, const void* v, int64_t stride_tok, int
         return FLOUR_ERR_UNSUPPORTED;
     }
     threads = (threads + 63) / 64 * 64;
-    const int64_t blocks = ((int64_t)num_tokens + tokens_per_block - 1) / tokens_per_block;
+    const int64_t per_block = (int64_t)tokens_per_block * KW_ROUNDS;
+    const int64_t blocks = ((int64_t)num_tokens + per_block - 1) / per_block;
     if (blocks > 0x7fffffff) {
         set_error("kv_write: too many tokens (%d)", num_tokens);
         return FLOUR_ERR_INVALID_ARGUMENT;
