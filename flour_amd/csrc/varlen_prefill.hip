@@ -511,6 +511,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 #pragma unroll
             for (int y = 0; y < 16; y++) st[mt][y] = 0.0f;
         __builtin_amdgcn_sched_barrier(0);
+        // The matrix sections run at raised wave priority: when both waves of a SIMD are ready,
+        // the one feeding MFMAs issues first and the other's VALU work fills behind it
+        // (measured +2% on the Llama-3-8B batch, +3.5% on the prefix batch).
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             st[0] = mfma32x32x16<T>(a0[kk], qb[kk], st[0]);
@@ -519,6 +523,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         }
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) st[1] = mfma32x32x16<T>(a1[kk], qb[kk], st[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
     };
     auto sm_pv = [&](int kt, int vbuf) __attribute__((always_inline)) {
         const int kv0 = kt * PF_KT;
@@ -586,6 +592,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 #pragma unroll
         for (int x = 0; x < 4; x++) weight(0, x);
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kk2 = 0; kk2 < 4; kk2++) {
 #pragma unroll
@@ -601,6 +608,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         lsum += psum;
     };
 
