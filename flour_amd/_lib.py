@@ -38,6 +38,10 @@ SIGNATURES: dict[str, tuple] = {
     "flour_hip_paged_decode": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _c_int,
                                         _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_f,
                                         _c_int, _vp, _c_sz, _vp]),
+    "flour_hip_paged_decode_noalloc_max_workspace": (_c_sz, []),
+    "flour_hip_paged_decode_noalloc": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp,
+                                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,
+                                                _c_int, _c_f, _c_int, _vp]),
     "flour_hip_varlen_prefill": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp,
                                           _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                           _c_int, _c_int, _c_int, _c_int, _c_i64, _c_f, _c_int,

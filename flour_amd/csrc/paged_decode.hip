@@ -41,6 +41,8 @@
 //    the end, and the accumulator is rescaled only when some lane's max moved.
 #include <math.h>
 
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "flour_common.h"
@@ -630,6 +632,56 @@ extern "C" int flour_hip_paged_decode_workspace_size(int batch, int num_heads, i
     return FLOUR_OK;
 }
 
+namespace flour {
+
+// Body of flour_hip_paged_decode. `workspace` == nullptr with `ws_from_scratch` set takes the
+// split-context workspace from this device's copy of `scratch` (flour_hip_paged_decode_noalloc).
+static int paged_decode_impl(void* out, int out_dtype, const void* q, const void* k_pool,
+                             const void* v_pool, const int32_t* block_tables,
+                             int max_blocks_per_seq, const int32_t* context_lens, int batch,
+                             int num_heads, int kv_heads, int head_dim, int block_size,
+                             int64_t num_slots, int max_context_len, float scale, int dtype,
+                             void* workspace, size_t workspace_bytes, bool ws_from_scratch,
+                             void* stream);
+
+// ------------------------------------------------------------------ allocation-free variant
+// The split-context workspace of flour_hip_paged_decode_noalloc lives in this file-scope device
+// array: each device the library runs on holds its own copy, for the life of the process. Host
+// code never passes the array's name to a kernel or a copy (on the host it is a stand-in, not a
+// device address): it uses the per-device address that hipGetSymbolAddress returns, looked up
+// once per device on that device's first call.
+static constexpr size_t DEC_SCRATCH_BYTES = (size_t)40 << 20;
+static __device__ __align__(256) unsigned char scratch[DEC_SCRATCH_BYTES];
+static constexpr int DEC_MAX_DEVICES = 64;
+static std::atomic<void*> g_scratch_ptr[DEC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int scratch_for_current_device(void** ptr) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return check_hip(e, "paged_decode_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= DEC_MAX_DEVICES) {
+        set_error("paged_decode_noalloc: device %d out of range", dev);
+        return FLOUR_ERR_UNSUPPORTED;
+    }
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (r != hipSuccess || !p)
+                return check_hip(r != hipSuccess ? r : hipErrorInvalidSymbol,
+                                 "paged_decode_noalloc: hipGetSymbolAddress(scratch)");
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *ptr = p;
+    return FLOUR_OK;
+}
+
+}  // namespace flour
+
 extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
                                       const void* k_pool, const void* v_pool,
                                       const int32_t* block_tables, int max_blocks_per_seq,
@@ -639,6 +691,41 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
                                       int dtype, void* workspace, size_t workspace_bytes,
                                       void* stream) {
     clear_error();
+    return flour::paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables,
+                                    max_blocks_per_seq, context_lens, batch, num_heads, kv_heads,
+                                    head_dim, block_size, num_slots, max_context_len, scale, dtype,
+                                    workspace, workspace_bytes, false, stream);
+}
+
+extern "C" size_t flour_hip_paged_decode_noalloc_max_workspace(void) {
+    return flour::DEC_SCRATCH_BYTES;
+}
+
+extern "C" int flour_hip_paged_decode_noalloc(void* out, int out_dtype, const void* q,
+                                              const void* k_pool, const void* v_pool,
+                                              const int32_t* block_tables,
+                                              int max_blocks_per_seq,
+                                              const int32_t* context_lens, int batch,
+                                              int num_heads, int kv_heads, int head_dim,
+                                              int block_size, int64_t num_slots,
+                                              int max_context_len, float scale, int dtype,
+                                              void* stream) {
+    clear_error();
+    return flour::paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables,
+                                    max_blocks_per_seq, context_lens, batch, num_heads, kv_heads,
+                                    head_dim, block_size, num_slots, max_context_len, scale, dtype,
+                                    nullptr, 0, true, stream);
+}
+
+namespace flour {
+
+static int paged_decode_impl(void* out, int out_dtype, const void* q, const void* k_pool,
+                             const void* v_pool, const int32_t* block_tables,
+                             int max_blocks_per_seq, const int32_t* context_lens, int batch,
+                             int num_heads, int kv_heads, int head_dim, int block_size,
+                             int64_t num_slots, int max_context_len, float scale, int dtype,
+                             void* workspace, size_t workspace_bytes, bool ws_from_scratch,
+                             void* stream) {
     if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) {
         set_error("paged_decode: unknown dtype (%d, out %d)", dtype, out_dtype);
         return FLOUR_ERR_INVALID_ARGUMENT;
@@ -676,6 +763,18 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
     }
     const int nwg = decode_workgroups();
     const size_t need = decode_ws_bytes(nwg, n_rep, head_dim, batch);
+    if (ws_from_scratch) {
+        if (need > DEC_SCRATCH_BYTES) {
+            set_error("paged_decode_noalloc: this call needs %zu bytes of split-context workspace, "
+                      "more than the %zu bytes of the library's scratch; use "
+                      "flour_hip_paged_decode with a caller workspace",
+                      need, DEC_SCRATCH_BYTES);
+            return FLOUR_ERR_WORKSPACE;
+        }
+        const int rc = scratch_for_current_device(&workspace);
+        if (rc != FLOUR_OK) return rc;
+        workspace_bytes = DEC_SCRATCH_BYTES;
+    }
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 256) != 0) {
         set_error("paged_decode: workspace of %zu bytes (256-byte aligned) required, got %zu "
                   "at %p",
@@ -711,3 +810,5 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
     FLOUR_DEC(f16_t);
 #undef FLOUR_DEC
 }
+
+}  // namespace flour

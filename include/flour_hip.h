@@ -130,6 +130,29 @@ int flour_hip_paged_decode(void* out, int out_dtype, const void* q, const void* 
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Paged decode with no allocation anywhere: flour_hip_paged_decode without the workspace
+ * arguments. This entry point has no counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). The split-context workspace comes from a device array inside the
+ * library, one per GPU (flour_hip_paged_decode_noalloc_max_workspace() bytes, 40 MiB, held
+ * until the process ends). Arguments, results and kernels are those of flour_hip_paged_decode.
+ * A call whose workspace would exceed that size fails with FLOUR_ERR_WORKSPACE before any
+ * launch (at 256 CUs every shape the MFMA path takes fits; larger GQA groups or batches than
+ * that would need flour_hip_paged_decode). Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (different streams, or threads without ordering) race
+ * and give wrong results. Nothing needs to start at zero; the array keeps the last call's
+ * contents.
+ * ---------------------------------------------------------------------------------------- */
+size_t flour_hip_paged_decode_noalloc_max_workspace(void);
+
+int flour_hip_paged_decode_noalloc(void* out, int out_dtype, const void* q, const void* k_pool,
+                                   const void* v_pool, const int32_t* block_tables,
+                                   int max_blocks_per_seq, const int32_t* context_lens,
+                                   int batch, int num_heads, int kv_heads, int head_dim,
+                                   int block_size, int64_t num_slots, int max_context_len,
+                                   float scale, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Kernel (3): causal varlen prefill attention over the paged cache.
  * Replaces paged_attention (src/backend/cpu.rs:57-112) for seq_q >= 1, batched over packed
  * sequences. Sequence s owns query rows cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1 and attends
