@@ -48,7 +48,7 @@ __global__ __launch_bounds__(GEN_THREADS) void attn_generic_kernel(
     int64_t q_sh, const TKV* __restrict__ k_pool, const TKV* __restrict__ v_pool,
     const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ block_tables, int max_blocks, int num_seqs, int n_rep,
-    int head_dim, int block_size, int64_t num_slots, float scale) {
+    int head_dim, int block_size, int64_t num_slots, int max_kv, float scale) {
     __shared__ float qs[512];
     __shared__ float ps[GEN_THREADS];
     __shared__ int64_t rows[GEN_THREADS];
@@ -77,7 +77,8 @@ __global__ __launch_bounds__(GEN_THREADS) void attn_generic_kernel(
         i = 0;
         q_len = 1;
     }
-    const int kv_len = min(kv_lens[s], max_blocks * block_size);  // never read past the table
+    // never read past the table; decode also clamps to max_context_len, as the MFMA path does
+    const int kv_len = min(min(kv_lens[s], max_blocks * block_size), max_kv);
     const int64_t n_vis = (kv_len >= q_len) ? (int64_t)kv_len - q_len + i + 1 : 0;
     const int kvh = h / n_rep;
     const int32_t* bt = block_tables + (int64_t)s * max_blocks;
@@ -135,12 +136,12 @@ static void launch_generic_t(void* out, int64_t o_st, int64_t o_sh, const void* 
                              int64_t q_sh, const void* k_pool, const void* v_pool,
                              const int32_t* cu, const int32_t* kv_lens, const int32_t* bt,
                              int max_blocks, int num_seqs, int total_q, int num_heads, int n_rep,
-                             int head_dim, int block_size, int64_t num_slots, float scale,
-                             hipStream_t stream) {
+                             int head_dim, int block_size, int64_t num_slots, int max_kv,
+                             float scale, hipStream_t stream) {
     attn_generic_kernel<TQ, TKV, TO><<<dim3(total_q, num_heads), dim3(GEN_THREADS), 0, stream>>>(
         static_cast<TO*>(out), o_st, o_sh, static_cast<const TQ*>(q), q_st, q_sh,
         static_cast<const TKV*>(k_pool), static_cast<const TKV*>(v_pool), cu, kv_lens, bt,
-        max_blocks, num_seqs, n_rep, head_dim, block_size, num_slots, scale);
+        max_blocks, num_seqs, n_rep, head_dim, block_size, num_slots, max_kv, scale);
 }
 
 template <typename T>
@@ -149,19 +150,19 @@ static void launch_generic_in(int out_dtype, void* out, int64_t o_st, int64_t o_
                               const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
                               const int32_t* bt, int max_blocks, int num_seqs, int total_q,
                               int num_heads, int n_rep, int head_dim, int block_size,
-                              int64_t num_slots, float scale, hipStream_t stream) {
+                              int64_t num_slots, int max_kv, float scale, hipStream_t stream) {
     if (out_dtype == FLOUR_DTYPE_F32)
         launch_generic_t<T, T, float>(out, o_st, o_sh, q, q_st, q_sh, k_pool, v_pool, cu, kv_lens,
                                       bt, max_blocks, num_seqs, total_q, num_heads, n_rep,
-                                      head_dim, block_size, num_slots, scale, stream);
+                                      head_dim, block_size, num_slots, max_kv, scale, stream);
     else if (out_dtype == FLOUR_DTYPE_BF16)
         launch_generic_t<T, T, bf16_t>(out, o_st, o_sh, q, q_st, q_sh, k_pool, v_pool, cu,
                                        kv_lens, bt, max_blocks, num_seqs, total_q, num_heads,
-                                       n_rep, head_dim, block_size, num_slots, scale, stream);
+                                       n_rep, head_dim, block_size, num_slots, max_kv, scale, stream);
     else
         launch_generic_t<T, T, f16_t>(out, o_st, o_sh, q, q_st, q_sh, k_pool, v_pool, cu, kv_lens,
                                       bt, max_blocks, num_seqs, total_q, num_heads, n_rep,
-                                      head_dim, block_size, num_slots, scale, stream);
+                                      head_dim, block_size, num_slots, max_kv, scale, stream);
 }
 
 // Launch the generic kernel; dtype is the storage type of q and the pools.
@@ -170,7 +171,7 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
                         const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
                         const int32_t* bt, int max_blocks, int num_seqs, int total_q,
                         int num_heads, int n_rep, int head_dim, int block_size, int64_t num_slots,
-                        float scale, hipStream_t stream) {
+                        int max_kv, float scale, hipStream_t stream) {
     if (head_dim > 512) {
         set_error("attention: head_dim %d > 512 is not supported", head_dim);
         return FLOUR_ERR_UNSUPPORTED;
@@ -183,15 +184,15 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
     if (dtype == FLOUR_DTYPE_F32)
         launch_generic_in<float>(out_dtype, out, o_st, o_sh, q, q_st, q_sh, k_pool, v_pool, cu,
                                  kv_lens, bt, max_blocks, num_seqs, total_q, num_heads, n_rep,
-                                 head_dim, block_size, num_slots, scale, stream);
+                                 head_dim, block_size, num_slots, max_kv, scale, stream);
     else if (dtype == FLOUR_DTYPE_BF16)
         launch_generic_in<bf16_t>(out_dtype, out, o_st, o_sh, q, q_st, q_sh, k_pool, v_pool, cu,
                                   kv_lens, bt, max_blocks, num_seqs, total_q, num_heads, n_rep,
-                                  head_dim, block_size, num_slots, scale, stream);
+                                  head_dim, block_size, num_slots, max_kv, scale, stream);
     else
         launch_generic_in<f16_t>(out_dtype, out, o_st, o_sh, q, q_st, q_sh, k_pool, v_pool, cu,
                                  kv_lens, bt, max_blocks, num_seqs, total_q, num_heads, n_rep,
-                                 head_dim, block_size, num_slots, scale, stream);
+                                 head_dim, block_size, num_slots, max_kv, scale, stream);
     return check_hip(hipGetLastError(), "attention (generic) launch");
 }
 

@@ -54,7 +54,7 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
                         const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
                         const int32_t* bt, int max_blocks, int num_seqs, int total_q,
                         int num_heads, int n_rep, int head_dim, int block_size, int64_t num_slots,
-                        float scale, hipStream_t stream);
+                        int max_kv, float scale, hipStream_t stream);
 
 static constexpr int DEC_D = 128;
 static constexpr float LOG2E = 1.4426950408889634f;
@@ -758,8 +758,8 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
         return launch_attn_generic(dtype, out_dtype, out, (int64_t)num_heads * head_dim, head_dim,
                                    q, (int64_t)num_heads * head_dim, head_dim, k_pool, v_pool,
                                    nullptr, context_lens, block_tables, max_blocks_per_seq, batch,
-                                   batch, num_heads, n_rep, head_dim, block_size, num_slots, scale,
-                                   s);
+                                   batch, num_heads, n_rep, head_dim, block_size, num_slots,
+                                   max_context_len, scale, s);
     }
     const int nwg = decode_workgroups();
     const size_t need = decode_ws_bytes(nwg, n_rep, head_dim, batch);

@@ -45,7 +45,7 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
                         const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
                         const int32_t* bt, int max_blocks, int num_seqs, int total_q,
                         int num_heads, int n_rep, int head_dim, int block_size, int64_t num_slots,
-                        float scale, hipStream_t stream);
+                        int max_kv, float scale, hipStream_t stream);
 
 static constexpr int PF_D = 128;
 static constexpr int PF_QT = 128;  // query rows per head per workgroup (4 waves x 32)
@@ -75,6 +75,22 @@ __device__ __forceinline__ int swap_bits01(int x) {
 //            one MFMA per product.
 //  PV_HILO:  P split into hi + lo parts of the storage type (~16 significant bits), V in the
 //            storage type; two MFMAs per product.
+//  exact:    the fallback of PV_F16 for an item whose fp16 P.V cannot be trusted (below):
+//            V stays bf16, P is split into bf16 hi + lo parts, and the running max is kept
+//            exact (no slack), so every weight is at most 1 and |p v| stays in fp32 range.
+//
+// bf16 V in PV_F16 mode is widened to fp16 as v * 2^8, which fp16 holds exactly for every bf16
+// value with 2^-25 <= |v| <= 255 (0 stays 0); the output is scaled back by 2^-8. Outside that:
+//  * |v| >= 256, inf or NaN widen to inf or NaN and make the accumulator non-finite;
+//  * 0 < |v| < 2^-25 is rounded to the fp16 grid, an error of at most 2^-33 in v, hence at most
+//    2^-33 in any output (the weights sum to 1).
+// At the end of each item every wave checks its 32 x 128 output block: if it is not finite, or
+// if its largest |output| is below 2^-16 (where 2^-33 per element could reach 5e-4 of the
+// block's L2 norm), the workgroup recomputes the item in exact mode. Otherwise the block's error
+// from the widening is at most 5e-4 of its norm and that from rounding P to fp16 ~1.5e-4.
+static constexpr float PF_V_SCALE = 256.0f;          // 2^8
+static constexpr float PF_V_UNSCALE = 1.0f / 256.0f;
+static constexpr float PF_MIN_TRUSTED = 0x1p-16f;   // smallest block max the fp16 path keeps
 enum { PV_F16 = 0, PV_HILO = 1 };
 
 static constexpr uint32_t PF_OOR = 0x80000000u;  // buffer offset past any pool: loads read 0
@@ -94,8 +110,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     constexpr int D = PF_D;
     // V^T is staged as fp16 for PV_F16, as the storage type otherwise; K keeps the storage type.
     typedef typename std::conditional<PV == PV_F16, f16_t, T>::type TV;
+    // bf16 V is widened to fp16 scaled by 2^8 and each item's output blocks are checked at its
+    // end (CHECK_V); a failed check recomputes the item in exact mode.
+    constexpr bool CHECK_V = PV == PV_F16 && std::is_same<T, bf16_t>::value;
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][PF_KT * PF_KPITCH];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][PF_D * PF_VPITCH];
+    __shared__ __attribute__((aligned(8))) uint8_t redo_flag[PF_WAVES];  // per wave, item end
 
     // ---- work items: (query tile, sequence, pair of query heads), ordered by decreasing
     // query-tile index ("level"): the cost of an item grows with its tile index (its causal kv
@@ -123,10 +143,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     __shared__ int sched_cum[PF_MAX_LEVELS + 2];   // [L]: items before level L
     __shared__ int sched_cu[PF_MAX_SEQS + 1];      // cu_seqlens
     __shared__ int sched_kv[PF_MAX_SEQS];          // clamped kv lengths
-    auto seq_tiles = [&](int sq) {  // query tiles of a sequence (0 if it cannot be served)
+    // query tiles of a sequence; one with kv_len < q_len still has its tiles, whose items
+    // attend nothing and write zero rows (as the generic path and the oracle do)
+    auto seq_tiles = [&](int sq) {
         const int l = sched_cu[sq + 1] - sched_cu[sq];
-        const int kl = sched_kv[sq];
-        return (l <= 0 || kl < l) ? 0 : min((l + PF_QT - 1) / PF_QT, NQ);
+        return l <= 0 ? 0 : min((l + PF_QT - 1) / PF_QT, NQ);
     };
     // exclusive suffix / prefix scans over up to PF_MAX_LEVELS + 1 entries by wave 0
     auto wave_scan = [&](int n, auto&& get, auto&& put, bool suffix) {
@@ -245,7 +266,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             const int qt = NQ - 1 - level;
             const int kvh = hp / pairs_per_kv;
             const int row_last = min(qt * PF_QT + PF_QT, ql) - 1;
-            const bool ok = qt * PF_QT < ql && kvl >= ql;  // always true for persistent items
+            const bool ok = qt * PF_QT < ql;  // always true for persistent items
             int* e = sched_items[k];
             e[0] = seq;
             e[1] = qt;
@@ -254,7 +275,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             e[4] = q0;
             e[5] = ql;
             e[6] = kvl;
-            e[7] = ok ? (kvl - ql + row_last + 1 + PF_KT - 1) / PF_KT : 0;  // causal kv tiles
+            // causal kv tiles; none when kv_len < q_len (the rows are written as zeros)
+            e[7] = (ok && kvl >= ql) ? (kvl - ql + row_last + 1 + PF_KT - 1) / PF_KT : 0;
             if (!persistent) sched_nitems = ok ? 1 : 0;
         }
         if (persistent && tid == 0) sched_nitems = n_items;
@@ -281,7 +303,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             it.ql = uni(b.y);
             it.kv_len = uni(b.z);
             it.n_kt = uni(b.w);
-            it.last_page = BS16 ? (it.kv_len - 1) >> 4 : (it.kv_len - 1) / block_size;
+            // (page 0 for an empty sequence: its loads are all masked, its table row exists)
+            it.last_page = it.kv_len > 0 ? (BS16 ? (it.kv_len - 1) >> 4 : (it.kv_len - 1) / block_size) : 0;
         }
         return it;
     };
@@ -354,7 +377,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         for (int i = 0; i < 4; i++) {
             const int tok0 = kt * PF_KT + 16 * i;
             const int lb = min(BS16 ? (tok0 >> 4) : tok0 / block_size, last_page);
-            const int idx = lb - wbase;  // < 64 for 16-token pages (a tile's 4 ids are aligned)
+            // < 64 for 16-token pages (a tile's 4 ids are aligned); negative only for the
+            // masked tiles before the first of an item with no kv tiles
+            const int idx = max(lb - wbase, 0);
             int id;
             if (BS16 || idx < 64) {
                 id = __builtin_amdgcn_readlane((int)win_cur, min(idx, 63));
@@ -383,17 +408,19 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             vd[j] = __builtin_amdgcn_raw_buffer_load_b128(
                 v_rsrc, 2 * v_tp + j < lim_rel ? vb + j * ROW_BYTES : PF_OOR, 0, BUF_NT);
     };
-    auto lds_store = [&](int buf, u32x4* kd, u32x4* vd) {
+    // `ex` true: exact mode, V is stored as bf16 without widening
+    auto lds_store = [&](auto ex, int buf, u32x4* kd, u32x4* vd) {
 #pragma unroll
         for (int i = 0; i < 2; i++)
             *reinterpret_cast<u32x4*>(&Ks[buf][(k_row + 32 * i) * PF_KPITCH + k_col]) = kd[i];
-        if constexpr (PV == PV_F16 && std::is_same<T, bf16_t>::value) {
-            // widen bf16 V to fp16 (exact inside the fp16 range)
+        if constexpr (CHECK_V && !decltype(ex)::value) {
+            // widen bf16 V to fp16 as v * 2^8 (exact for 2^-25 <= |v| <= 255 and 0)
 #pragma unroll
             for (int j = 0; j < 2; j++)
 #pragma unroll
                 for (int x = 0; x < 4; x++)
-                    vd[j][x] = pack2<f16_t>(lo_f32<bf16_t>(vd[j][x]), hi_f32<bf16_t>(vd[j][x]));
+                    vd[j][x] = pack2<f16_t>(lo_f32<bf16_t>(vd[j][x]) * PF_V_SCALE,
+                                            hi_f32<bf16_t>(vd[j][x]) * PF_V_SCALE);
         }
         const int col = sigma16(2 * v_tp);  // the pair stays adjacent under sigma16
 #pragma unroll
@@ -430,6 +457,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         for (int kk = 0; kk < 8; kk++) qb[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
     };
 
+    float out_scale = 1.0f;  // 2^-8 after the fp16 path over bf16 V (CHECK_V), else 1
     // Running state: the reference max m may lag the true running max by up to
     // PF_RESCALE_SLACK (weights then reach 2^8), which skips most accumulator rescales.
     float m = -INFINITY, lsum = 0.0f;
@@ -446,7 +474,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     auto store_output = [&]() __attribute__((always_inline)) {
         const float l = lsum + wave_shfl_xor(lsum, 32);
         if (wave_active) {
-            const float inv = 1.0f / l;
+            // 0: an item that attends nothing; out_scale undoes the widening scale of V
+            const float inv = l > 0.0f ? out_scale / l : 0.0f;
             if constexpr (sizeof(TO) == 4) {
                 const int orow = wr0 + ql32;
                 if (orow < ql) {
@@ -526,10 +555,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
-    auto sm_pv = [&](int kt, int vbuf) __attribute__((always_inline)) {
+    // ---- mask, tile max and lazy rescale of tile kt's scores; `slack` is how far (in log2
+    // units) the reference max may lag the running max.
+    auto softmax_max = [&](int kt, float slack) __attribute__((always_inline)) {
         const int kv0 = kt * PF_KT;
-        // ---- mask, on tiles that cross the diagonal of some row of this wave only. The empty
-        // asm statements keep the compiler from if-converting these uniform branches into
+        // mask, on tiles that cross the diagonal of some row of this wave only. The empty asm
+        // statements keep the compiler from if-converting these uniform branches into
         // per-element selects on every tile.
         if (kv0 + PF_KT - 1 > wave_min_lim) {
             asm volatile("" ::: "memory");
@@ -542,14 +573,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                     for (int j = 0; j < 4; j++)
                         if (32 * mt + 8 * i + j > tl) st[mt][4 * i + j] = -INFINITY;
         }
-        // ---- tile max of the raw scores (scale > 0, so the max commutes with the scaling)
+        // tile max of the raw scores (scale > 0, so the max commutes with the scaling)
         float tm[2] = {-INFINITY, -INFINITY};
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int y = 0; y < 16; y += 2) tm[mt] = vmax(vmax(tm[mt], st[mt][y]), st[mt][y + 1]);
         const float tmax = max_across_halves(vmax(tm[0], tm[1])) * scale_log2;
-        if (__builtin_amdgcn_ballot_w64(tmax > m + PF_RESCALE_SLACK) != 0) {
+        if (__builtin_amdgcn_ballot_w64(tmax > m + slack) != 0) {
             asm volatile("" ::: "memory");
             const float m_new = fmaxf(m, tmax);
             const float alpha = fast_exp2(m - m_new);
@@ -558,6 +589,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             for (int x = 0; x < 4; x++) o[x] *= alpha;
             m = m_new;
         }
+    };
+    auto sm_pv = [&](int kt, int vbuf) __attribute__((always_inline)) {
+        softmax_max(kt, PF_RESCALE_SLACK);
         // ---- p = 2^(s * scale_log2 - m), one FMA + exp per score, packed as the P^T B operand
         // of step kk2 (tokens of half kk2/2, rows i = 2(kk2&1), +1); then O^T += V^T P^T in
         // kk2-major order, so that the exps of step kk2+1 and the V reads of step kk2+1 can run
@@ -611,6 +645,36 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         __builtin_amdgcn_s_setprio(0);
         lsum += psum;
     };
+    // Exact-mode softmax and P.V of tile kt over a bf16 V^T tile: exact running max, P split
+    // into bf16 hi + lo, one k-step at a time (the rare path; few live registers).
+    auto sm_pv_exact = [&](int kt, int vbuf) __attribute__((always_inline)) {
+        softmax_max(kt, 0.0f);
+        const float nm = -m;
+        float psum = 0.0f;
+        const uint16_t* vr = &Vt[vbuf][ql32 * PF_VPITCH + 8 * h2];
+#pragma unroll
+        for (int kk2 = 0; kk2 < 4; kk2++) {
+            const int mt = kk2 >> 1, y0 = 8 * (kk2 & 1);
+            u32x4 ph, pl;
+#pragma unroll
+            for (int x = 0; x < 4; x++) {
+                const float a0 = fast_exp2(fmaf(st[mt][y0 + 2 * x], scale_log2, nm));
+                const float a1 = fast_exp2(fmaf(st[mt][y0 + 2 * x + 1], scale_log2, nm));
+                const uint32_t hi = pack2<T>(a0, a1);
+                ph[x] = hi;
+                pl[x] = pack2<T>(a0 - lo_f32<T>(hi), a1 - hi_f32<T>(hi));
+                psum += a0 + a1;
+            }
+#pragma unroll
+            for (int mt2 = 0; mt2 < 4; mt2++) {
+                const u32x4 vv = *reinterpret_cast<const u32x4*>(vr + 32 * mt2 * PF_VPITCH + 16 * kk2);
+                o[mt2] = mfma32x32x16<T>(vv, ph, o[mt2]);
+                o[mt2] = mfma32x32x16<T>(vv, pl, o[mt2]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        lsum += psum;
+    };
 
     // ---- items: while the epilogue of one item stores its output, the Q rows and the first
     // two K / V tiles of the next one are already in flight. Within an item, one barrier per
@@ -619,44 +683,67 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     if (n_items == 0) return;
     u32x4 ka[2], va[2], kb[2], vb[2];
     int pb0[4], pb1[4], pb2[4];
-    auto prologue = [&](const Item& it, const Item& after) __attribute__((always_inline)) {
-        set_load(it);
-        load_q(it);
-        win_cur = win_pre;
+    // the first tiles of the item in the load context: tiles 0 and 1 in flight, page ids of
+    // tile 2 ready, the block-table windows at the start (win_cur must hold entries 0..63)
+    auto start_tiles = [&]() __attribute__((always_inline)) {
         wbase = 0;
         ld_ok = false;
         win_next = load_window(bt, 64, last_page + 1);
-        if (after.valid)  // first window of the item after this one
-            win_pre = load_window(block_tables + (int64_t)after.seq * max_blocks, 0,
-                                  after.last_page + 1);
         page_bases(0, pb0);
         gload(0, pb0, true, ka, va);
         page_bases(min(1, n_kt - 1), pb1);
         gload(1, pb1, 1 < n_kt, kb, vb);
         page_bases(min(2, n_kt - 1), pb2);
     };
+    auto prologue = [&](const Item& it, const Item& after) __attribute__((always_inline)) {
+        set_load(it);
+        load_q(it);
+        win_cur = win_pre;
+        if (after.valid)  // first window of the item after this one
+            win_pre = load_window(block_tables + (int64_t)after.seq * max_blocks, 0,
+                                  after.last_page + 1);
+        start_tiles();
+    };
+    // Item-end check of the fp16 path (CHECK_V): true if this wave's output block is not finite
+    // or its largest |output| is below PF_MIN_TRUSTED (both in the 2^8-scaled accumulator:
+    // |o| / l is 2^8 times the output).
+    auto block_untrusted = [&]() __attribute__((always_inline)) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 4; x++)
+#pragma unroll
+            for (int y = 0; y < 16; y += 2)
+                mx = vmax(vmax(mx, __builtin_fabsf(o[x][y])), __builtin_fabsf(o[x][y + 1]));
+        const float l = lsum + wave_shfl_xor(lsum, 32);
+        const bool nonfinite = !(mx < INFINITY);  // NaN compares false
+        const bool big = mx >= PF_MIN_TRUSTED * PF_V_SCALE * l;
+        return wave_active && (__builtin_amdgcn_ballot_w64(nonfinite) != 0 ||
+                               __builtin_amdgcn_ballot_w64(big) == 0);
+    };
     Item ci = fetch(0);
     win_pre = load_window(block_tables + (int64_t)ci.seq * max_blocks, 0, ci.last_page + 1);
     prologue(ci, fetch(1));
     set_compute(ci);
     for (int k = 0;;) {
-        reset_state();
-        // Q must have landed before the loop (its loads precede the tile loads, so this waits
-        // for them alone); otherwise the compiler sinks the Q loads past the first barrier and
-        // keeps a conservative wait for them inside the loop
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++) asm volatile("" ::"v"(qb[kk]));
-        lds_store(0, ka, va);
-        __syncthreads();
-        // step kt: refill `nx` with tile kt + 2, compute tile kt, store tile kt + 1 (in `st1`)
-        auto step = [&](int kt, u32x4* knx, u32x4* vnx, u32x4* kst1, u32x4* vst1) {
+        // step kt: refill `nx` with tile kt + 2, compute tile kt, store tile kt + 1 (in `st1`).
+        // `ex`: exact mode. On the fp16 path the last step records this wave's item-end check
+        // before its barrier, which publishes it.
+        auto step = [&](auto ex, int kt, u32x4* knx, u32x4* vnx, u32x4* kst1,
+                        u32x4* vst1) __attribute__((always_inline)) {
+            constexpr bool EX = decltype(ex)::value;
             gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
             page_bases(min(kt + 3, n_kt - 1), pb0);
             if (visible(kt)) {
                 qk(kt & 1);
-                sm_pv(kt, kt & 1);
+                if constexpr (EX)
+                    sm_pv_exact(kt, kt & 1);
+                else
+                    sm_pv(kt, kt & 1);
             }
-            lds_store((kt + 1) & 1, kst1, vst1);
+            if constexpr (CHECK_V && !EX) {
+                if (kt == n_kt - 1) redo_flag[w] = block_untrusted() ? 1 : 0;
+            }
+            lds_store(ex, (kt + 1) & 1, kst1, vst1);
 #pragma unroll
             for (int i = 0; i < 4; i++) {  // pb2 <- tile kt + 3
                 const int x = pb2[i];
@@ -665,9 +752,35 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
             __syncthreads();
         };
-        for (int kt = 0; kt < n_kt; kt += 2) {
-            step(kt, ka, va, kb, vb);
-            if (kt + 1 < n_kt) step(kt + 1, kb, vb, ka, va);
+        // all tiles of the current item, from tiles 0 and 1 in flight (start_tiles)
+        auto run_tiles = [&](auto ex) __attribute__((always_inline)) {
+            reset_state();
+            // Q must have landed before the loop (its loads precede the tile loads, so this
+            // waits for them alone); otherwise the compiler sinks the Q loads past the first
+            // barrier and keeps a conservative wait for them inside the loop
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) asm volatile("" ::"v"(qb[kk]));
+            lds_store(ex, 0, ka, va);
+            __syncthreads();
+            for (int kt = 0; kt < n_kt; kt += 2) {
+                step(ex, kt, ka, va, kb, vb);
+                if (kt + 1 < n_kt) step(ex, kt + 1, kb, vb, ka, va);
+            }
+        };
+        run_tiles(std::false_type{});
+        if constexpr (CHECK_V) {
+            out_scale = PF_V_UNSCALE;
+            bool redo = false;
+            if (n_kt > 0) {  // flags written before the last step's barrier
+                const u32x2 f = *reinterpret_cast<const u32x2*>(&redo_flag[0]);
+                redo = uni((int)(f[0] | f[1])) != 0;
+            }
+            if (redo) {  // the whole item again in exact mode (every wave, uniform branch)
+                win_cur = load_window(bt, 0, last_page + 1);
+                start_tiles();
+                run_tiles(std::true_type{});
+                out_scale = 1.0f;
+            }
         }
         const Item nx = fetch(++k);
         if (nx.valid) prologue(nx, fetch(k + 1));
@@ -782,7 +895,8 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
         return launch_attn_generic(dtype, out_dtype, out, o_stride_tok, o_stride_head, q,
                                    q_stride_tok, q_stride_head, k_pool, v_pool, cu_seqlens_q,
                                    kv_lens, block_tables, max_blocks_per_seq, num_seqs, total_q,
-                                   num_heads, n_rep, head_dim, block_size, num_slots, scale, s);
+                                   num_heads, n_rep, head_dim, block_size, num_slots, INT_MAX,
+                                   scale, s);
     }
 #define FLOUR_PF(T, TO)                                                                          \
     return g_prefill_pv_mode == PV_HILO                                                          \

@@ -21,8 +21,12 @@
  *     (kv_heads, num_slots, head_dim) row-major, exactly as PagedKvPool::new builds them
  *     (paged.rs:124-167). Slot s of physical block b is b * block_size + s % block_size
  *     (paged.rs:114-116), so the 16 rows of one (head, block) pair are contiguous.
- *   - Element types are given by the flour_dtype codes below. Arithmetic is fp32 throughout;
- *     bf16/f16 inputs are widened exactly, outputs are rounded to nearest-even.
+ *   - Element types are given by the flour_dtype codes below. Scores, softmax and accumulators
+ *     are fp32 and outputs are rounded to nearest-even. The matrix products take bf16/f16
+ *     inputs exactly, with one exception: prefill over bf16 pools runs P.V on fp16 matrix
+ *     cores with V widened as v * 2^8 (exact for 2^-25 <= |v| <= 255) and P rounded to fp16;
+ *     a work item whose output is not finite or is all below 2^-16 in magnitude is recomputed
+ *     with bf16 V and P split into two bf16 parts. Decode splits P into two 16-bit parts.
  */
 #ifndef FLOUR_HIP_H
 #define FLOUR_HIP_H
@@ -67,6 +71,10 @@ const char* flour_hip_version(void);
  * stride_tok = kv_heads*head_dim, stride_head = head_dim.
  * A negative slot marks a padding token and is skipped; a slot >= num_slots is never written.
  * The copy is bit-exact (no conversion): k/v and the pools share `dtype`.
+ * Each non-negative slot may appear at most once per call (BlockTable::slots, paged.rs:118-121,
+ * never repeats one): tokens are written in parallel, so for a repeated slot the stored row is
+ * one of the repeating tokens' rows, chosen 16 bytes at a time, not the last token's. The cache
+ * layers of flour_cache.h only build mappings without repeats.
  * ---------------------------------------------------------------------------------------- */
 int flour_hip_kv_write(const void* k, const void* v, int64_t stride_tok, int64_t stride_head,
                        void* k_pool, void* v_pool, const int32_t* slot_mapping, int num_tokens,
@@ -108,7 +116,8 @@ int flour_hip_rope_kv_write(void* q_out, const void* q, int64_t q_stride_tok,
  *   q            (batch, num_heads, head_dim) contiguous, post-RoPE
  *   out          (batch, num_heads, head_dim) contiguous, element type out_dtype
  *   block_tables [batch, max_blocks_per_seq] int32 physical block ids, logical order
- *   context_lens [batch] int32 kv length of each sequence (>= 1; 0 gives a zero row)
+ *   context_lens [batch] int32 kv length of each sequence (>= 1; 0 gives a zero row; a
+ *                length above max_context_len attends the first max_context_len positions)
  *   Query head h attends kv head h / (num_heads / kv_heads) (repeat_kv, cpu.rs:5-13).
  *   scale multiplies q.k before the softmax (attention.rs:108 passes 1/sqrt(head_dim)).
  *   max_context_len bounds context_lens[] and sizes the split-context grid.
@@ -162,7 +171,8 @@ int flour_hip_paged_decode_noalloc(void* out, int out_dtype, const void* q, cons
  *
  *   q    row r, head h at r*q_stride_tok + h*q_stride_head (elements), head_dim contiguous
  *   out  row r, head h at r*o_stride_tok + h*o_stride_head, element type out_dtype
- *   cu_seqlens_q [num_seqs+1] int32, kv_lens [num_seqs] int32 (kv_len >= q_len)
+ *   cu_seqlens_q [num_seqs+1] int32, kv_lens [num_seqs] int32 (kv_len >= q_len; a sequence
+ *                with kv_len < q_len attends nothing and its rows are written as zeros)
  *   block_tables [num_seqs, max_blocks_per_seq] int32
  *   max_seqlen_q bounds the per-sequence query count; total_q = cu_seqlens_q[num_seqs].
  * The K/V of the new rows must already be in the pool (flour_hip_kv_write).

@@ -7,7 +7,8 @@ Tolerances (written here, per the path's contract):
                                      oracle (the kernel's fp32 accumulator, before rounding);
   * bf16 pools, bf16 output:         exactly RNE(kernel fp32 result); rel-L2 within 5% of the
                                      floor set by rounding the exact result to bf16 (~1.5e-3,
-                                     above the fp32 limit), max-abs within floor + 2e-3.
+                                     above the fp32 limit), max-abs within floor + 2e-3, and
+                                     within 1 bf16 ulp of RNE(reference) where |ref| >= 2^-10.
 """
 from __future__ import annotations
 
@@ -16,7 +17,7 @@ import pytest
 import torch
 
 import oracle as O
-from _util import check_bf16_output, errors, to_np
+from _util import DECODE_ULP_BOUNDS, check_bf16_output, errors, to_np
 from flour_amd import ops
 from flour_amd.workloads import make_decode, make_workload
 
@@ -43,7 +44,7 @@ def check_bf16(c, tag=""):
     max_abs, rel = errors(got32, ref)
     print(f"{tag} fp32-out max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
-    rep = check_bf16_output(to_np(run(c, torch.bfloat16)), got32, ref)
+    rep = check_bf16_output(to_np(run(c, torch.bfloat16)), got32, ref, DECODE_ULP_BOUNDS)
     print(f"{tag} bf16-out {rep}", flush=True)
     return max_abs, rel
 
@@ -215,3 +216,48 @@ def test_decode_batch_beyond_the_mfma_limit_uses_the_generic_kernel(device):
                             np.arange(5001, dtype=np.int32), to_np(d.context_lens), 16, d.scale)
     max_abs, rel = errors(to_np(out), ref)
     assert max_abs <= 2e-3 and rel <= 1e-3, (max_abs, rel)
+
+
+def test_decode_context_beyond_max_context_len_is_clamped_on_every_path(device):
+    """context_lens[b] above max_context_len attends the first max_context_len positions, on
+    the MFMA path (bf16) and on the generic path (fp32 pools) alike."""
+    for dt, tol in ((torch.bfloat16, 2e-3), (torch.float32, 1e-5)):
+        c = make_decode(3, 8, 2, 128, 16, (1, 1), dtype=dt, seed=5, device=device,
+                        context_lens=[300, 700, 40])
+        out = ops.paged_decode(c.q, c.k_pool, c.v_pool, c.block_tables, c.context_lens, c.scale,
+                               500, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        clamped = np.minimum(to_np(c.context_lens), 500).astype(np.int32)
+        ref = O.paged_attention(to_np(c.q), to_np(c.k_pool), to_np(c.v_pool),
+                                to_np(c.block_tables), np.arange(4, dtype=np.int32), clamped, 16,
+                                c.scale, bf16=True)
+        max_abs, _ = errors(to_np(out), ref)
+        assert max_abs <= tol, (dt, max_abs)
+
+
+def test_decode_v_far_from_unit_scale(device):
+    """V rows of +-1e5, one of +-3e38 per sequence and rows of 1e-30 among N(0, 1) rows: the
+    decode P.V runs in the pool's own type (bf16 V is never narrowed) with an exact running
+    max, so every weight is at most 1. Judged relative to the output scale."""
+    c = make_decode(4, 16, 4, 128, 16, (1, 1), dtype=torch.bfloat16, seed=8, device=device,
+                    context_lens=[900, 37, 2000, 513])
+    vp = c.v_pool.float()
+    g = torch.Generator(device="cpu").manual_seed(9)
+    for b, n in enumerate(c.context_lens.tolist()):
+        pos = torch.randperm(n, generator=g)[:6]
+        sl = [int(c.block_tables[b, p // 16]) * 16 + int(p) % 16 for p in pos]
+        vp[:, sl[0], :] = 3e38 * torch.sign(vp[:, sl[0], :])
+        for s_ in sl[1:3]:
+            vp[:, s_, :] *= 1e5
+        for s_ in sl[3:]:
+            vp[:, s_, :] = 1e-30
+    c.v_pool.copy_(vp.to(torch.bfloat16))
+    ref = oracle_decode(c)
+    got = to_np(run(c, torch.float32))
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin)
+    scale = float(np.abs(ref[fin]).max())
+    max_abs, rel = errors(got[fin] / scale, ref[fin] / scale)
+    print(f"decode V far from unit scale: scale={scale:.3e} max_abs={max_abs:.3e} rel={rel:.3e}",
+          flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
