@@ -525,16 +525,18 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // S^T of the tile in flight (64 tokens x 32 queries, two 32-token halves, raw q.k).
     f32x16 st[2];
     auto visible = [&](int kt) { return wave_active && kt * PF_KT <= wave_lim; };  // per wave
-    auto qk = [&](int kbuf) __attribute__((always_inline)) {
-        // ---- S^T tile (64 tokens x 32 queries) in two 32-token halves, raw q.k. Issue order,
-        // pinned with scheduling fences: the first half's eight K reads, then each product of
-        // the first half followed by one K read of the second half, then the second half's
-        // products (every read is in flight for at least one product).
-        const uint16_t* kr0 = &Ks[kbuf][ql32 * PF_KPITCH + 8 * h2];
-        const uint16_t* kr1 = kr0 + 32 * PF_KPITCH;
-        u32x4 a0[8], a1[8];
+    // ---- S^T tile (64 tokens x 32 queries) in two 32-token halves, raw q.k: 16 products in
+    // kk-major order alternating the halves (two independent accumulation chains), K fragments
+    // read four products ahead. `fill` is work independent of the scores (the staging of the
+    // next tile) that the products are interleaved with.
+    auto qk = [&](int kbuf, auto&& fill) __attribute__((always_inline)) {
+        const uint16_t* kr = &Ks[kbuf][ql32 * PF_KPITCH + 8 * h2];
+        auto frag = [&](int i) {  // product i: half i & 1, dims 16 (i >> 1) .. of the K rows
+            return *reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * PF_KPITCH + 16 * (i >> 1));
+        };
+        u32x4 fr[16];
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++) a0[kk] = *reinterpret_cast<const u32x4*>(kr0 + 16 * kk);
+        for (int i = 0; i < 4; i++) fr[i] = frag(i);
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -544,14 +546,19 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         // the one feeding MFMAs issues first and the other's VALU work fills behind it
         // (measured +2% on the Llama-3-8B batch, +3.5% on the prefix batch).
         __builtin_amdgcn_s_setprio(1);
+        fill();
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++) {
-            st[0] = mfma32x32x16<T>(a0[kk], qb[kk], st[0]);
-            a1[kk] = *reinterpret_cast<const u32x4*>(kr1 + 16 * kk);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 16; i++) {
+            if (i + 4 < 16) fr[i + 4] = frag(i + 4);
+            st[i & 1] = mfma32x32x16<T>(fr[i], qb[i >> 1], st[i & 1]);
         }
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++) st[1] = mfma32x32x16<T>(a1[kk], qb[kk], st[1]);
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a K fragment read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to three VALU
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // up to one LDS write
+        }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
@@ -734,7 +741,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
             page_bases(min(kt + 3, n_kt - 1), pb0);
             if (visible(kt)) {
-                qk(kt & 1);
+                qk(kt & 1, [] {});
                 if constexpr (EX)
                     sm_pv_exact(kt, kt & 1);
                 else
