@@ -390,6 +390,33 @@ def cpu_prefill_baseline(case, seconds: float):
     return case.flops() / med / 1e12, threads, len(times)
 
 
+def _dtype_names():
+    import torch
+
+    return {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+class _LazyNames(dict):
+    def __missing__(self, key):
+        self.update(_dtype_names())
+        return dict.__getitem__(self, key)
+
+
+DTYPE_NAME = _LazyNames()
+
+
+def decode_kernel_name(case) -> str:
+    """Which kernel the library runs for a decode case (its dispatch rule, restated)."""
+    import torch
+
+    B, H, D = case.q.shape
+    G = case.k_pool.shape[0]
+    mfma = (case.q.dtype in (torch.bfloat16, torch.float16) and D == 128 and
+            case.block_size % 16 == 0 and H // G <= 16 and B <= 4096)
+    return ("paged_decode_mfma_kernel + paged_decode_merge_kernel" if mfma
+            else "attn_simt_kernel (vector ALUs)")
+
+
 def bench_decode(torch, ops, case, steps, warmup, graph: bool = False):
     """Times decode steps. With graph=True the step (main + merge kernel) is captured once in a
     HIP graph and replayed, as a serving loop would, which removes the host launch overhead;
@@ -599,19 +626,19 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": DTYPE_NAME[case.q.dtype],
         "data": "synthetic (seeded N(0,1); block tables a random permutation of a 1.25x pool)",
         "config": {
             "workload": name, "batch": cfg["batch"], "num_heads": cfg["num_heads"],
             "kv_heads": cfg["kv_heads"], "head_dim": cfg["head_dim"],
             "block_size": cfg["block_size"], "context_lens": f"U[{cfg['ctx'][0]},{cfg['ctx'][1]}]",
             "total_context_tokens": int(case.context_lens.sum().item()),
-            "algorithmic_bytes_per_step": r["bytes"], "out_dtype": "bf16",
+            "algorithmic_bytes_per_step": r["bytes"], "out_dtype": DTYPE_NAME[case.q.dtype],
             "pool_copies": r["copies"],
             "launch": "HIP graph replay of the step" if args.graph else "eager",
         },
         "roofline": {
-            "bound": "hbm", "kernel": "paged_decode_mfma_kernel + paged_decode_merge_kernel",
+            "bound": "hbm", "kernel": decode_kernel_name(case),
             "achieved": round(r["gbs_kernel"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
             "avg_launch_us": round(r["kernel_ms"] * 1e3, 3),
@@ -636,16 +663,23 @@ def main():
     if not args.no_extra:
         extra = {}
         for nm, c in WORKLOADS.items():
-            if nm == name or nm.startswith("decode_f32"):
+            if nm == name:
                 continue
             cs = make_workload(nm, device=dev)
             torch.cuda.synchronize()
             if c["kind"] == "decode":
                 rr = bench_decode(torch, ops, cs, args.steps, args.warmup)
-                extra[nm] = {"GB/s": round(rr["gbs_kernel"], 1),
-                             "hbm_frac": round(rr["gbs_kernel"] / HBM_PEAK_GBS, 4),
-                             "avg_launch_us": round(rr["kernel_ms"] * 1e3, 2),
-                             "algorithmic_bytes": rr["bytes"]}
+                e = {"GB/s": round(rr["gbs_kernel"], 1),
+                     "hbm_frac": round(rr["gbs_kernel"] / HBM_PEAK_GBS, 4),
+                     "avg_launch_us": round(rr["kernel_ms"] * 1e3, 2),
+                     "algorithmic_bytes": rr["bytes"],
+                     "kernel": decode_kernel_name(cs)}
+                if not args.no_cpu:
+                    med, th, reps = cpu_decode_baseline(cs, 3.0)
+                    e["cpu_GB/s"] = round(rr["bytes"] / med / 1e9, 3)
+                    e["cpu_sample"] = f"whole batch, median of {reps} runs, {th} threads"
+                    e["speedup"] = round(rr["gbs_kernel"] / (rr["bytes"] / med / 1e9), 1)
+                extra[nm] = e
             else:
                 rr = bench_prefill(torch, ops, cs, args.steps, args.warmup, ROPE_THETA.get(nm, 500000.0))
                 e = {"TFLOP/s": round(rr["tflops"], 1),

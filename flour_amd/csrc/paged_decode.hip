@@ -49,6 +49,14 @@
 
 namespace flour {
 
+bool simt_supported(int dtype, int head_dim, const void* q, int64_t q_st, int64_t q_sh,
+                    const void* k_pool, const void* v_pool);
+int launch_attn_simt(int dtype, int out_dtype, void* out, int64_t o_st, int64_t o_sh,
+                     const void* q, int64_t q_st, int64_t q_sh, const void* k_pool,
+                     const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
+                     const int32_t* bt, int max_blocks, int num_seqs, int total_q, int num_heads,
+                     int n_rep, int head_dim, int block_size, int64_t num_slots, int max_kv,
+                     float scale, hipStream_t stream);
 int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64_t o_sh,
                         const void* q, int64_t q_st, int64_t q_sh, const void* k_pool,
                         const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
@@ -755,6 +763,12 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
                       ((uintptr_t)v_pool % 16 == 0);
     if (!mfma) {
         // one query row per sequence: cu_seqlens == nullptr
+        const int64_t qs = (int64_t)num_heads * head_dim;
+        if (simt_supported(dtype, head_dim, q, qs, head_dim, k_pool, v_pool))
+            return launch_attn_simt(dtype, out_dtype, out, qs, head_dim, q, qs, head_dim, k_pool,
+                                    v_pool, nullptr, context_lens, block_tables,
+                                    max_blocks_per_seq, batch, batch, num_heads, n_rep, head_dim,
+                                    block_size, num_slots, max_context_len, scale, s);
         return launch_attn_generic(dtype, out_dtype, out, (int64_t)num_heads * head_dim, head_dim,
                                    q, (int64_t)num_heads * head_dim, head_dim, k_pool, v_pool,
                                    nullptr, context_lens, block_tables, max_blocks_per_seq, batch,

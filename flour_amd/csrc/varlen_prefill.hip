@@ -40,6 +40,14 @@
 
 namespace flour {
 
+bool simt_supported(int dtype, int head_dim, const void* q, int64_t q_st, int64_t q_sh,
+                    const void* k_pool, const void* v_pool);
+int launch_attn_simt(int dtype, int out_dtype, void* out, int64_t o_st, int64_t o_sh,
+                     const void* q, int64_t q_st, int64_t q_sh, const void* k_pool,
+                     const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
+                     const int32_t* bt, int max_blocks, int num_seqs, int total_q, int num_heads,
+                     int n_rep, int head_dim, int block_size, int64_t num_slots, int max_kv,
+                     float scale, hipStream_t stream);
 int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64_t o_sh,
                         const void* q, int64_t q_st, int64_t q_sh, const void* k_pool,
                         const void* v_pool, const int32_t* cu, const int32_t* kv_lens,
@@ -899,6 +907,12 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
                       num_slots % block_size == 0 && scale > 0.0f &&
                       num_slots * head_dim * 2 <= (int64_t)0x7fffffff;
     if (!mfma) {
+        if (simt_supported(dtype, head_dim, q, q_stride_tok, q_stride_head, k_pool, v_pool))
+            return launch_attn_simt(dtype, out_dtype, out, o_stride_tok, o_stride_head, q,
+                                    q_stride_tok, q_stride_head, k_pool, v_pool, cu_seqlens_q,
+                                    kv_lens, block_tables, max_blocks_per_seq, num_seqs, total_q,
+                                    num_heads, n_rep, head_dim, block_size, num_slots, INT_MAX,
+                                    scale, s);
         return launch_attn_generic(dtype, out_dtype, out, o_stride_tok, o_stride_head, q,
                                    q_stride_tok, q_stride_head, k_pool, v_pool, cu_seqlens_q,
                                    kv_lens, block_tables, max_blocks_per_seq, num_seqs, total_q,

@@ -17,6 +17,8 @@ N(0, 1) unless stated):
                                 adds a U[128, 512]-token suffix; 28 q / 4 kv heads
   decode_bf16_long_llama3_70b   long-context decode, bf16: batch 8, 64 q / 8 kv heads,
                                 context U[16384, 32768]
+  decode_bf16_qwen25_05b        bf16 decode at head_dim 64 (the Qwen2.5-0.5B-Instruct attention
+                                shape): batch 64, 14 q / 2 kv heads, context U[512, 4096]
 
 Physical blocks are a seeded random permutation of a pool 1.25x the blocks needed.
 """
@@ -43,6 +45,8 @@ WORKLOADS: dict[str, dict] = {
     "decode_bf16_long_llama3_70b": dict(kind="decode", batch=8, num_heads=64, kv_heads=8,
                                         head_dim=128, block_size=16, ctx=(16384, 32768),
                                         dtype=torch.bfloat16, seed=5),
+    "decode_bf16_qwen25_05b": dict(kind="decode", batch=64, num_heads=14, kv_heads=2, head_dim=64,
+                                   block_size=16, ctx=(512, 4096), dtype=torch.bfloat16, seed=6),
 }
 
 

@@ -261,3 +261,29 @@ def test_decode_v_far_from_unit_scale(device):
     print(f"decode V far from unit scale: scale={scale:.3e} max_abs={max_abs:.3e} rel={rel:.3e}",
           flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+@pytest.mark.parametrize("dt,H,G,D,bs,ctx", [
+    (torch.float32, 8, 8, 64, 16, [1, 2, 255, 256]),     # the fp32 decode workload's shape
+    (torch.float32, 16, 2, 128, 16, [1000, 3]),          # fp32 at head_dim 128, n_rep 8
+    (torch.float32, 32, 2, 32, 7, [77, 500]),            # n_rep 16: two head groups; odd pages
+    (torch.float32, 4, 4, 256, 16, [300]),               # one lane group per wave
+    (torch.bfloat16, 14, 2, 64, 16, [1, 900, 2049]),     # Qwen2.5-0.5B attention shape
+    (torch.float16, 8, 4, 64, 32, [33, 700]),
+    (torch.bfloat16, 8, 2, 16, 16, [5, 130]),            # two lanes per row
+])
+def test_decode_vector_kernel_shapes(device, dt, H, G, D, bs, ctx):
+    """Shapes the matrix-core decode does not take (fp32 pools, head_dim != 128, any page
+    size) run on the vector kernel: fp32 max-abs <= 1e-5, 16-bit pools 2e-3 / 1e-3."""
+    c = make_decode(len(ctx), H, G, D, bs, (1, 1), dtype=dt, seed=H * D + bs, device=device,
+                    context_lens=ctx)
+    got = to_np(run(c, torch.float32))
+    ref = O.paged_attention(to_np(c.q), to_np(c.k_pool), to_np(c.v_pool), to_np(c.block_tables),
+                            np.arange(len(ctx) + 1, dtype=np.int32), to_np(c.context_lens), bs,
+                            c.scale, bf16=(dt != torch.float16))
+    max_abs, rel = errors(got, ref)
+    print(f"vector decode {dt} H={H} G={G} D={D}: max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    if dt == torch.float32:
+        assert max_abs <= 1e-5
+    else:
+        assert max_abs <= 2e-3 and rel <= 1e-3

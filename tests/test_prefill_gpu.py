@@ -351,3 +351,26 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     max_abs, rel = errors(to_np(a)[rows], ref)
     print(f"persistent H={H} G={G} max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+@pytest.mark.parametrize("dt,H,G,D,bs,lens,prefix", [
+    (torch.float32, 8, 8, 64, 16, [1, 17, 40, 300], 32),   # eight rows per workgroup
+    (torch.float32, 16, 4, 128, 16, [129, 5], 0),           # two rows x four heads
+    (torch.float32, 16, 1, 32, 7, [50, 1], 14),             # n_rep 16: two head groups
+    (torch.bfloat16, 14, 2, 64, 16, [300, 77, 1], 64),      # Qwen2.5-0.5B attention shape
+    (torch.float16, 8, 2, 64, 32, [90, 33], 32),
+])
+def test_prefill_vector_kernel_shapes(device, dt, H, G, D, bs, lens, prefix):
+    """Shapes the matrix-core prefill does not take run on the vector kernel: fp32 max-abs
+    <= 1e-5 against the oracle, 16-bit pools 2e-3 / 1e-3 (fp32 output)."""
+    c = make_prefill(len(lens), H, G, D, bs, (1, 1), prefix=prefix, dtype=dt, seed=H + D,
+                     device=device, q_lens=lens)
+    write(c)
+    ref, rows = oracle_prefill(c)
+    got = to_np(run(c, torch.float32))[rows]
+    max_abs, rel = errors(got, ref)
+    print(f"vector prefill {dt} H={H} G={G} D={D}: max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
+    if dt == torch.float32:
+        assert max_abs <= 1e-5
+    else:
+        assert max_abs <= 2e-3 and rel <= 1e-3
