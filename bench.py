@@ -411,7 +411,7 @@ def decode_kernel_name(case) -> str:
 
     B, H, D = case.q.shape
     G = case.k_pool.shape[0]
-    mfma = (case.q.dtype in (torch.bfloat16, torch.float16) and D == 128 and
+    mfma = (case.q.dtype in (torch.bfloat16, torch.float16) and D in (64, 128) and
             case.block_size % 16 == 0 and H // G <= 16 and B <= 4096)
     return ("paged_decode_mfma_kernel + paged_decode_merge_kernel" if mfma
             else "attn_simt_kernel (vector ALUs)")

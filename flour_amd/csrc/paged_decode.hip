@@ -64,7 +64,6 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
                         int num_heads, int n_rep, int head_dim, int block_size, int64_t num_slots,
                         int max_kv, float scale, hipStream_t stream);
 
-static constexpr int DEC_D = 128;
 static constexpr float LOG2E = 1.4426950408889634f;
 
 static constexpr int DEC_CHUNK = 32;         // tokens per step (two 16-token MFMA tiles)
@@ -76,7 +75,8 @@ static constexpr int DEC_WAVES_PER_CU = 8;  // 2 per SIMD: the register budget o
 // K directly in that layout takes a 64 B quarter of 16 rows per instruction, a pattern that
 // streams at most ~6.0 TB/s from HBM against ~6.8 TB/s for whole rows (measured with the same
 // 2048-wave, double-buffered access over random 4 KB runs).
-static constexpr int DEC_KPITCH = 272;  // bytes per K row in LDS: conflict-free writes and reads
+// Bytes per K row in LDS (head_dim 128 / 64): conflict-free 16-byte fragment reads of 16 rows.
+__host__ __device__ constexpr int dec_kpitch(int d) { return d == 128 ? 272 : 144; }
 
 struct DecodeWs {
     float* ml;  // [2 * num_waves][n_rep][2] (max, sum) in the exp2 domain
@@ -125,16 +125,22 @@ __device__ __forceinline__ int64_t owner_wg(int64_t x, int64_t total, int64_t n)
     return ((x + 1) * n + total - 1) / total - 1;
 }
 
-// One wave per workgroup; each wave owns one contiguous range of the chunk list.
-template <typename T, typename TO, bool BS16>
+// One wave per workgroup; each wave owns one contiguous range of the chunk list. D is the head
+// dim, 128 or 64. A lane's K/V share of a 16-token tile is rows 4lg .. 4lg + 3 at 16-byte
+// (D 128: dims 8lc ..) or 8-byte (D 64: dims 4lc ..) width, so a wave reads whole rows.
+template <typename T, typename TO, bool BS16, int D>
 __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     TO* __restrict__ out, const T* __restrict__ q, const T* __restrict__ k_pool,
     const T* __restrict__ v_pool, const int32_t* __restrict__ block_tables, int max_blocks,
     const int32_t* __restrict__ context_lens, int batch, int num_heads, int kv_heads, int n_rep,
     int block_size, int64_t num_slots, int max_ctx, float scale_log2, DecodeWs ws) {
-    constexpr int D = DEC_D;
+    static_assert(D == 128 || D == 64, "matrix-core decode: head_dim 128 or 64");
+    constexpr int KP = dec_kpitch(D);
+    constexpr int NV = D / 16;  // O^T products per chunk (16 output dims each)
+    // a lane's load of one row: 8 (D 128) or 4 (D 64) dims
+    typedef typename std::conditional<D == 128, u32x4, u32x2>::type Ld;
     extern __shared__ int pre[];  // pre[b] = chunks of sequences 0..b-1; pre[batch] = all
-    __shared__ __attribute__((aligned(16))) unsigned char kt[16 * DEC_KPITCH];  // one K tile
+    __shared__ __attribute__((aligned(16))) unsigned char kt[16 * KP];  // one K tile
     const int lane = threadIdx.x, lg = lane >> 4, lc = lane & 15;
 
     // ---- exclusive prefix sum of per-sequence chunk counts (each lane scans a slice)
@@ -171,8 +177,8 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     if (lo >= hi) return;
 
     const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
-    // K and V: instruction j of a tile reads rows 4lg + j, dims 8lc .. 8lc + 7 (4 whole rows)
-    const uint32_t v_off = (uint32_t)((4 * lg * D + 8 * lc) * sizeof(T));
+    // K and V: instruction j of a tile reads rows 4lg + j, dims (D / 16) lc .. (4 whole rows)
+    const uint32_t v_off = (uint32_t)((4 * lg * D + (D / 16) * lc) * sizeof(T));
     const int64_t max_phys = num_slots / block_size - 1;
 
     // The wave's range is a stream of segments: up to DEC_SEG consecutive chunks of one
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // loop-invariant lane offset (VGPR) and the tile's byte offset (SGPR), so there is no
     // per-lane address arithmetic in the loop; non-temporal (K/V are read exactly once);
     // an out-of-region offset reads zeros instead of faulting.
-    auto load_chunk = [&](int g, Slots sl, int tile0, u32x4 (*kd)[4], u32x4 (*vd)[4]) {
+    auto load_chunk = [&](int g, Slots sl, int tile0, Ld (*kd)[4], Ld (*vd)[4]) {
         const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(k_pool + (int64_t)g * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
         const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -234,30 +240,40 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
                 (uint32_t)(id * block_size + __builtin_amdgcn_readlane(sl.off, tile0 + t)) *
                 (uint32_t)(D * sizeof(T));
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                kd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
-                    k_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
+            for (int j = 0; j < 4; j++) {
+                if constexpr (D == 128)
+                    kd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                        k_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
+                else
+                    kd[t][j] = __builtin_amdgcn_raw_buffer_load_b64(
+                        k_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
+            }
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                vd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
-                    v_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
+            for (int j = 0; j < 4; j++) {
+                if constexpr (D == 128)
+                    vd[t][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                        v_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
+                else
+                    vd[t][j] = __builtin_amdgcn_raw_buffer_load_b64(
+                        v_rsrc, v_off + j * D * (uint32_t)sizeof(T), soff, BUF_NT);
+            }
         }
     };
     // Q^T as the B operand: lane (lg, lc) holds head lc, dims 32kk + 8lg .. +7.
-    u32x4 qb[4];
+    u32x4 qb[D / 32];
     auto load_q = [&](int b, int g) {
         const T* qh = q + ((int64_t)b * num_heads + (int64_t)g * n_rep + lc) * D + 8 * lg;
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++)
+        for (int kk = 0; kk < D / 32; kk++)
             qb[kk] = (lc < n_rep) ? *reinterpret_cast<const u32x4*>(qh + 32 * kk) : u32x4{0, 0, 0, 0};
     };
 
     float m = -INFINITY, lsum = 0.0f;
-    f32x4 acc[8];
+    f32x4 acc[NV];
 #pragma unroll
-    for (int nn = 0; nn < 8; nn++) acc[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nn = 0; nn < NV; nn++) acc[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute_chunk = [&](int c, int tok_end, u32x4 (*ka)[4], u32x4 (*va)[4]) {
+    auto compute_chunk = [&](int c, int tok_end, Ld (*ka)[4], Ld (*va)[4]) {
         const int tok0 = c * DEC_CHUNK;
         const bool full = tok0 + DEC_CHUNK <= tok_end;
         if (!full) {  // tokens past the context: zero V so garbage bits cannot leak in
@@ -265,23 +281,23 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (tok0 + 16 * t + 4 * lg + j >= tok_end) va[t][j] = u32x4{0, 0, 0, 0};
+                    if (tok0 + 16 * t + 4 * lg + j >= tok_end) va[t][j] = Ld{};
         }
         // K rows through LDS into the A-operand layout: lane (lg, lc) needs row lc, dims
         // 32kk + 8lg .. +7. One wave per workgroup and LDS operations of a wave complete in
         // order, so the wave barriers only keep the compiler from moving LDS accesses across.
         // The second tile's writes follow the first tile's reads in that order.
-        u32x4 kA[2][4];
+        u32x4 kA[2][D / 32];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                *reinterpret_cast<u32x4*>(&kt[(4 * lg + j) * DEC_KPITCH + 16 * lc]) = ka[t][j];
+                *reinterpret_cast<Ld*>(&kt[(4 * lg + j) * KP + (int)sizeof(Ld) * lc]) = ka[t][j];
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-                kA[t][kk] = *reinterpret_cast<const u32x4*>(&kt[lc * DEC_KPITCH + 64 * kk + 16 * lg]);
+            for (int kk = 0; kk < D / 32; kk++)
+                kA[t][kk] = *reinterpret_cast<const u32x4*>(&kt[lc * KP + 64 * kk + 16 * lg]);
         }
         __builtin_amdgcn_wave_barrier();
         // S tiles: s[t][r] = score of head lc for token 16t + 4lg + r of the chunk.
@@ -290,7 +306,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
         for (int t = 0; t < 2; t++) {
             s[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) s[t] = mfma16x16x32<T>(kA[t][kk], qb[kk], s[t]);
+            for (int kk = 0; kk < D / 32; kk++) s[t] = mfma16x16x32<T>(kA[t][kk], qb[kk], s[t]);
         }
         float sv[8];
         float tmax = -INFINITY;
@@ -312,7 +328,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
                (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
         if (__builtin_amdgcn_ballot_w64(m_new > m) != 0) {
 #pragma unroll
-            for (int nn = 0; nn < 8; nn++) acc[nn] *= alpha;
+            for (int nn = 0; nn < NV; nn++) acc[nn] *= alpha;
         }
         m = m_new;
         // P^T as the B operand over the 32 tokens: lane (lg, lc) holds head lc at
@@ -325,10 +341,10 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
             PH[i] = hi16;
             PL[i] = pack2<T>(p[2 * i] - lo_f32<T>(hi16), p[2 * i + 1] - hi_f32<T>(hi16));
         }
-        // V^T as the A operand: lane (lg, lc) holds output dim 8lc + nn at the same
+        // V^T as the A operand: lane (lg, lc) holds output dim (D / 16) lc + nn at the same
         // k-slots, packed in-lane from its four V rows of each tile.
 #pragma unroll
-        for (int nn = 0; nn < 8; nn++) {
+        for (int nn = 0; nn < NV; nn++) {
             const int wd = nn >> 1;
             u32x4 A;
 #pragma unroll
@@ -346,38 +362,42 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
         }
     };
 
-    // Piece epilogue from registers: lane (lg, lc) holds head lc, dims 32lg + 8r + nn.
+    // Piece epilogue from registers: lane (lg, lc) holds head lc, dims (D / 4) lg + NV r + nn
+    // (r < 4, nn < NV): D / 4 contiguous dims.
     auto epilogue = [&](int b, int g, bool complete, bool first_piece) {
         lsum = sum_across_rows(lsum);
         if (lc < n_rep) {
             if (complete) {  // whole pair in this range: final output
-                TO* o = out + ((int64_t)b * num_heads + (int64_t)g * n_rep + lc) * D + 32 * lg;
+                TO* o = out + ((int64_t)b * num_heads + (int64_t)g * n_rep + lc) * D + (D / 4) * lg;
                 const float inv = 1.0f / lsum;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     if constexpr (sizeof(TO) == 4) {
-                        *reinterpret_cast<f32x4*>(o + 8 * r) =
-                            f32x4{acc[0][r] * inv, acc[1][r] * inv, acc[2][r] * inv, acc[3][r] * inv};
-                        *reinterpret_cast<f32x4*>(o + 8 * r + 4) =
-                            f32x4{acc[4][r] * inv, acc[5][r] * inv, acc[6][r] * inv, acc[7][r] * inv};
-                    } else {
-                        u32x4 v;
 #pragma unroll
-                        for (int i = 0; i < 4; i++)
+                        for (int h4 = 0; h4 < NV; h4 += 4)
+                            *reinterpret_cast<f32x4*>(o + NV * r + h4) =
+                                f32x4{acc[h4][r] * inv, acc[h4 + 1][r] * inv, acc[h4 + 2][r] * inv,
+                                      acc[h4 + 3][r] * inv};
+                    } else {
+                        uint32_t v[NV / 2];
+#pragma unroll
+                        for (int i = 0; i < NV / 2; i++)
                             v[i] = pack2<TO>(acc[2 * i][r] * inv, acc[2 * i + 1][r] * inv);
-                        *reinterpret_cast<u32x4*>(o + 8 * r) = v;
+                        if constexpr (NV == 8)
+                            *reinterpret_cast<u32x4*>(o + NV * r) = u32x4{v[0], v[1], v[2], v[3]};
+                        else
+                            *reinterpret_cast<u32x2*>(o + NV * r) = u32x2{v[0], v[1]};
                     }
                 }
             } else {  // partial row for the merge kernel
                 const int64_t pidx = (2 * wgi + (first_piece ? 0 : 1)) * n_rep + lc;
-                float* o = ws.o + pidx * D + 32 * lg;
+                float* o = ws.o + pidx * D + (D / 4) * lg;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    *reinterpret_cast<f32x4*>(o + 8 * r) =
-                        f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-                    *reinterpret_cast<f32x4*>(o + 8 * r + 4) =
-                        f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
-                }
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int h4 = 0; h4 < NV; h4 += 4)
+                        *reinterpret_cast<f32x4*>(o + NV * r + h4) =
+                            f32x4{acc[h4][r], acc[h4 + 1][r], acc[h4 + 2][r], acc[h4 + 3][r]};
                 if (lg == 0) {
                     ws.ml[2 * pidx] = m;
                     ws.ml[2 * pidx + 1] = lsum;
@@ -387,7 +407,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
         m = -INFINITY;
         lsum = 0.0f;
 #pragma unroll
-        for (int nn = 0; nn < 8; nn++) acc[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int nn = 0; nn < NV; nn++) acc[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     };
 
     // ---- the chunk stream. The next segment's block-table slots are read while the current
@@ -413,8 +433,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // One stream step: prefetch the chunk after c into (kn, vn) (PREFETCH is a compile-time
     // constant at each call, so the steady-state loop has no conditional loads), compute c
     // from (kc, vc), then advance the cursor.
-    auto step = [&](auto prefetch, u32x4 (*kc)[4], u32x4 (*vc)[4], u32x4 (*kn)[4],
-                    u32x4 (*vn)[4]) {
+    auto step = [&](auto prefetch, Ld (*kc)[4], Ld (*vc)[4], Ld (*kn)[4], Ld (*vn)[4]) {
         const bool seg_end = c + 1 >= cur.ce;
         // At a segment's last chunk the segment after the next one is looked up and its
         // block-table entries are requested before this step's chunk loads, so the rotation at
@@ -465,7 +484,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
 
     using pf_on = std::integral_constant<bool, true>;
     using pf_off = std::integral_constant<bool, false>;
-    u32x4 ka[2][4], va[2][4], kb[2][4], vb[2][4];
+    Ld ka[2][4], va[2][4], kb[2][4], vb[2][4];
     load_chunk(cur.g, cur_slots, 0, ka, va);
     int64_t remaining = hi - lo;  // chunks this wave computes; all but the last prefetch one
     for (; remaining > 2; remaining -= 2) {
@@ -487,18 +506,19 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
 // lane accumulates its two dims over the batch with independent loads, reading each piece's
 // weight and slot from the lane that holds it; batches combine with the same online rescaling
 // as the running update of cpu.rs:96-105. No LDS and no barrier.
-template <typename TO>
+template <typename TO, int D>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     TO* __restrict__ out, int batch, int num_heads, int kv_heads, int n_rep, int nwg_i,
     DecodeWs ws) {
-    constexpr int D = DEC_D;
+    // lane i owns output dims E i .. E i + E - 1
+    constexpr int E = D / 64;
     const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     // chunks before sequence b, of sequence b and in all sequences (the main kernel's sums)
     const int before = ws.pre[b], nch = ws.pre[b + 1] - before, all = ws.pre[batch];
-    TO* o = out + ((int64_t)b * num_heads + h) * D + 2 * lane;
+    TO* o = out + ((int64_t)b * num_heads + h) * D + E * lane;
     if (nch == 0) {
-        o[0] = from_f32<TO>(0.0f);
-        o[1] = from_f32<TO>(0.0f);
+#pragma unroll
+        for (int i = 0; i < E; i++) o[i] = from_f32<TO>(0.0f);
         return;
     }
     const int g = h / n_rep, hh = h - g * n_rep;
@@ -523,7 +543,9 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     if (f == l) return;  // finished inside one wave range
     const int np = (int)(l - f + 1);  // ranges f..l; empty ones wrote nothing
 
-    float M = -INFINITY, L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+    float M = -INFINITY, L = 0.0f, O[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) O[i] = 0.0f;
     const int fslot = (int)(f_first ? 2 * f : 2 * f + 1);  // the first piece always exists
     // Wave ranges can be empty only when there are fewer chunks than waves; otherwise skip the
     // (64-bit, slow) range-bound divisions.
@@ -533,13 +555,22 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
         if (!dense && ij * total / nwg == (ij + 1) * total / nwg) return -1;
         return (int)((ij == f && !f_first) ? 2 * ij + 1 : 2 * ij);
     };
-    auto row = [&](int slot) -> f32x2 {  // this lane's two dims of a piece's partial row
-        return *reinterpret_cast<const f32x2*>(ws.o + ((int64_t)slot * n_rep + hh) * D + 2 * lane);
+    typedef typename std::conditional<E == 2, f32x2, float>::type RowV;
+    auto row = [&](int slot) -> RowV {  // this lane's E dims of a piece's partial row
+        return *reinterpret_cast<const RowV*>(ws.o + ((int64_t)slot * n_rep + hh) * D + E * lane);
+    };
+    auto add = [&](float wj, RowV v) {
+        if constexpr (E == 2) {
+            O[0] += wj * v[0];
+            O[1] += wj * v[1];
+        } else {
+            O[0] += wj * v;
+        }
     };
     for (int p0 = 0; p0 < np; p0 += 64) {
         // The batch's first 8 pieces' rows are loaded before the (max, sum) reductions, which
         // they do not depend on (a missing piece reads the first piece's row, weight 0).
-        f32x2 v0[8];
+        RowV v0[8];
         int s0[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -560,22 +591,19 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
         for (int off = 32; off > 0; off >>= 1) bl += __shfl_xor(bl, off, 64);
         const float c_old = (M == -INFINITY) ? 0.0f : fast_exp2(M - m_new);
         L = L * c_old + bl;
-        O0 *= c_old;
-        O1 *= c_old;
+#pragma unroll
+        for (int i = 0; i < E; i++) O[i] *= c_old;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const float wj = __shfl(w, j, 64);
-            if (s0[j] >= 0) {
-                O0 += wj * v0[j][0];
-                O1 += wj * v0[j][1];
-            }
+            if (s0[j] >= 0) add(wj, v0[j]);
         }
         // The rest in groups of 8 unconditional loads (a missing piece reads the first piece's
         // row) so they are all in flight together; the select drops them, so stale workspace
         // bits (even NaN) never reach the sum.
         const int nb = min(64, np - p0);
         for (int q = 8; q < nb; q += 8) {
-            f32x2 v[8];
+            RowV v[8];
             int sl[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
@@ -585,36 +613,48 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const float wj = __shfl(w, q + j, 64);
-                if (sl[j] >= 0) {
-                    O0 += wj * v[j][0];
-                    O1 += wj * v[j][1];
-                }
+                if (sl[j] >= 0) add(wj, v[j]);
             }
         }
         M = m_new;
     }
-    o[0] = from_f32<TO>(O0 / L);
-    o[1] = from_f32<TO>(O1 / L);
+#pragma unroll
+    for (int i = 0; i < E; i++) o[i] = from_f32<TO>(O[i] / L);
 }
 
-template <typename T, typename TO>
-static int launch_decode_mfma(void* out, const void* q, const void* k_pool, const void* v_pool,
-                              const int32_t* bt, int max_blocks, const int32_t* ctx_lens,
-                              int batch, int num_heads, int kv_heads, int n_rep, int block_size,
-                              int64_t num_slots, int max_ctx, float scale, int nwg, DecodeWs ws,
-                              hipStream_t stream) {
+template <typename T, typename TO, int D>
+static int launch_decode_mfma_d(void* out, const void* q, const void* k_pool, const void* v_pool,
+                                const int32_t* bt, int max_blocks, const int32_t* ctx_lens,
+                                int batch, int num_heads, int kv_heads, int n_rep, int block_size,
+                                int64_t num_slots, int max_ctx, float scale, int nwg, DecodeWs ws,
+                                hipStream_t stream) {
     const size_t lds = (size_t)(batch + 1) * sizeof(int);
-    auto kern = block_size == 16 ? paged_decode_mfma_kernel<T, TO, true>
-                                 : paged_decode_mfma_kernel<T, TO, false>;
+    auto kern = block_size == 16 ? paged_decode_mfma_kernel<T, TO, true, D>
+                                 : paged_decode_mfma_kernel<T, TO, false, D>;
     kern<<<dim3(nwg), dim3(64), lds, stream>>>(
         static_cast<TO*>(out), static_cast<const T*>(q), static_cast<const T*>(k_pool),
         static_cast<const T*>(v_pool), bt, max_blocks, ctx_lens, batch, num_heads, kv_heads, n_rep,
         block_size, num_slots, max_ctx, scale * LOG2E, ws);
     int rc = check_hip(hipGetLastError(), "paged_decode launch");
     if (rc != FLOUR_OK) return rc;
-    paged_decode_merge_kernel<TO><<<dim3(num_heads, batch), dim3(64), 0, stream>>>(
+    paged_decode_merge_kernel<TO, D><<<dim3(num_heads, batch), dim3(64), 0, stream>>>(
         static_cast<TO*>(out), batch, num_heads, kv_heads, n_rep, nwg, ws);
     return check_hip(hipGetLastError(), "paged_decode merge launch");
+}
+
+template <typename T, typename TO>
+static int launch_decode_mfma(int head_dim, void* out, const void* q, const void* k_pool,
+                              const void* v_pool, const int32_t* bt, int max_blocks,
+                              const int32_t* ctx_lens, int batch, int num_heads, int kv_heads,
+                              int n_rep, int block_size, int64_t num_slots, int max_ctx,
+                              float scale, int nwg, DecodeWs ws, hipStream_t stream) {
+    if (head_dim == 64)
+        return launch_decode_mfma_d<T, TO, 64>(out, q, k_pool, v_pool, bt, max_blocks, ctx_lens,
+                                               batch, num_heads, kv_heads, n_rep, block_size,
+                                               num_slots, max_ctx, scale, nwg, ws, stream);
+    return launch_decode_mfma_d<T, TO, 128>(out, q, k_pool, v_pool, bt, max_blocks, ctx_lens,
+                                            batch, num_heads, kv_heads, n_rep, block_size,
+                                            num_slots, max_ctx, scale, nwg, ws, stream);
 }
 
 }  // namespace flour
@@ -756,7 +796,7 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int n_rep = num_heads / kv_heads;
     const bool mfma = (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
-                      head_dim == DEC_D && block_size % 16 == 0 && n_rep <= 16 &&
+                      (head_dim == 128 || head_dim == 64) && block_size % 16 == 0 && n_rep <= 16 &&
                       batch <= DEC_MAX_BATCH && num_heads <= 65535 &&
                       num_slots * head_dim * 2 <= (int64_t)0x7fffffff &&
                       ((uintptr_t)q % 16 == 0) && ((uintptr_t)k_pool % 16 == 0) &&
@@ -805,17 +845,17 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
 #define FLOUR_DEC(T)                                                                            \
     do {                                                                                        \
         if (out_dtype == FLOUR_DTYPE_F32)                                                       \
-            return launch_decode_mfma<T, float>(out, q, k_pool, v_pool, block_tables,           \
+            return launch_decode_mfma<T, float>(head_dim, out, q, k_pool, v_pool, block_tables,           \
                                                 max_blocks_per_seq, context_lens, batch,        \
                                                 num_heads, kv_heads, n_rep, block_size,         \
                                                 num_slots, max_context_len, scale, nwg, ws, s); \
         if (out_dtype == FLOUR_DTYPE_BF16)                                                      \
-            return launch_decode_mfma<T, bf16_t>(out, q, k_pool, v_pool, block_tables,          \
+            return launch_decode_mfma<T, bf16_t>(head_dim, out, q, k_pool, v_pool, block_tables,          \
                                                  max_blocks_per_seq, context_lens, batch,       \
                                                  num_heads, kv_heads, n_rep, block_size,        \
                                                  num_slots, max_context_len, scale, nwg, ws,    \
                                                  s);                                            \
-        return launch_decode_mfma<T, f16_t>(out, q, k_pool, v_pool, block_tables,               \
+        return launch_decode_mfma<T, f16_t>(head_dim, out, q, k_pool, v_pool, block_tables,               \
                                             max_blocks_per_seq, context_lens, batch, num_heads, \
                                             kv_heads, n_rep, block_size, num_slots,             \
                                             max_context_len, scale, nwg, ws, s);                \

@@ -287,3 +287,22 @@ def test_decode_vector_kernel_shapes(device, dt, H, G, D, bs, ctx):
         assert max_abs <= 1e-5
     else:
         assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+@pytest.mark.parametrize("H,G,ctx", [
+    (14, 2, [1, 2, 15, 16, 17, 31, 63, 64, 65, 100]),   # n_rep 7, partial tiles
+    (8, 8, [1000, 513, 2049]),                          # n_rep 1, several splits
+    (32, 2, [3000, 5]),                                 # n_rep 16
+])
+def test_decode_bf16_mfma_head_dim_64(device, H, G, ctx):
+    """The matrix-core decode at head_dim 64 (Qwen2.5-0.5B-sized heads): 8-byte lane loads,
+    K through the LDS tile, V^T packed in-lane, 16-dim output blocks."""
+    c = make_decode(len(ctx), H, G, 64, 16, (1, 1), dtype=torch.bfloat16, seed=H + G + 64,
+                    device=device, context_lens=ctx)
+    check_bf16(c, f"D=64 H={H} G={G}")
+
+
+def test_decode_head_dim_64_workload(device):
+    """bf16 decode, batch 64, 14 q / 2 kv heads, head_dim 64, contexts U[512, 4096]."""
+    c = make_workload("decode_bf16_qwen25_05b", device=device)
+    check_bf16(c, "qwen2.5-0.5b decode")
