@@ -673,6 +673,7 @@ def main():
                      "hbm_frac": round(rr["gbs_kernel"] / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(rr["kernel_ms"] * 1e3, 2),
                      "algorithmic_bytes": rr["bytes"],
+                     "traffic": read_traffic(nm),
                      "kernel": decode_kernel_name(cs)}
                 if not args.no_cpu:
                     med, th, reps = cpu_decode_baseline(cs, 3.0)
@@ -685,6 +686,8 @@ def main():
                 e = {"TFLOP/s": round(rr["tflops"], 1),
                      "mfma_frac": round(rr["tflops"] / BF16_PEAK_TFLOPS, 4),
                      "attn_us": round(rr["attn_ms"] * 1e3, 2), "flops": rr["flops"],
+                     "traffic": read_traffic(nm),
+                     "kv_write_traffic": read_traffic(nm.replace("prefill_", "kv_write_")),
                      "kv_write_GB/s": round(rr["write_gbs"], 1),
                      "kv_write_us": round(rr["write_ms"] * 1e3, 2),
                      "rope_kv_write_GB/s": round(rr["rope_gbs"], 1),
