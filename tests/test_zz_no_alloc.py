@@ -92,3 +92,35 @@ def test_noalloc_rejects_a_workspace_beyond_its_scratch(device):
     assert "scratch" in _lib.last_error()
     torch.cuda.synchronize()
     assert bool((out == 0).all())
+
+
+def test_noalloc_graph_replay_matches_eager(device):
+    """The allocation-free call captured in a HIP graph (the use it exists for) and replayed,
+    with eager allocation-free calls of another batch between replays (they rewrite the shared
+    scratch), gives the eager result bit for bit on every replay."""
+    c = make_decode(16, 32, 8, 128, 16, (1, 3000), dtype=torch.bfloat16, seed=44, device=device)
+    other = make_decode(5, 28, 4, 128, 16, (1, 2000), dtype=torch.bfloat16, seed=45,
+                        device=device)
+    eager = noalloc(c)
+    other_ref = noalloc(other)
+    out = torch.empty(c.q.shape, dtype=torch.float32, device=device)
+    lib = _lib.lib()
+
+    def step():
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.flour_hip_paged_decode_noalloc(*_args(c, out), stream))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for i in range(4):
+        out.zero_()
+        assert torch.equal(noalloc(other), other_ref), f"eager call before replay {i} differs"
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs"
