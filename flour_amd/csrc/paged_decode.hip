@@ -9,7 +9,7 @@
 //
 // Work decomposition (stream-K at wave granularity): the K/V to read is the list of 32-token
 // chunks of every (sequence, kv head) pair, laid end to end. One resident round of one-wave
-// workgroups (4 per CU, 1 per SIMD) each takes an equal contiguous range of that list, so every
+// workgroups (3 per CU) each takes an equal contiguous range of that list, so every
 // wave streams the same number of bytes whatever the spread of context lengths, and no wave
 // pays a launch or a ramp-up twice. A pair wholly inside one range is finished by its wave; a
 // pair cut by range ends leaves one partial (max, sum, acc) row per piece, and a small second
@@ -69,12 +69,13 @@ static constexpr float LOG2E = 1.4426950408889634f;
 static constexpr int DEC_CHUNK = 32;         // tokens per step (two 16-token MFMA tiles)
 static constexpr int DEC_SEG = 32;           // chunks per tile-slot refill (64 tiles, one per lane)
 static constexpr int DEC_MAX_BATCH = 4096;   // per-sequence chunk prefix sums live in LDS
-// One wave per SIMD. Each wave keeps one 32-token chunk in flight while it computes the
-// previous one (16 KB at head_dim 128), so 1024 waves hold ~16 MB of reads, about HBM's
-// bandwidth-delay product; twice as many waves only lengthen the queues and open more DRAM
-// rows at once on the random 4 KB page runs (measured: 4 waves per CU stream 3-7% faster than
-// 8 on the Llama-3-8B / 70B / Qwen2.5-0.5B decode batches, 5 per CU are slower than either).
-static constexpr int DEC_WAVES_PER_CU = 4;
+// Three waves per CU. Each wave keeps one 32-token chunk in flight while it computes the
+// previous one (16 KB at head_dim 128), so 768 waves hold ~12 MB of reads, about HBM's
+// bandwidth-delay product; more waves only lengthen the queues and open more DRAM rows at once
+// on the random 4 KB page runs (measured on the Llama-3-8B / 70B / Qwen2.5-0.5B decode batches:
+// 3 per CU stream 0.3-1.5% faster than 4, which stream 3-7% faster than 8; counts that do not
+// divide evenly over a CU's 4 SIMDs, 2.5, 3.5 and 5 per CU, are slower than their neighbours).
+static constexpr int DEC_WAVES_PER_CU = 3;
 // K is read like V, four whole 256 B rows per instruction with the non-temporal hint, and
 // turned into the MFMA A-operand layout (row = lane % 16) through a per-wave LDS tile. Reading
 // K directly in that layout takes a 64 B quarter of 16 rows per instruction, a pattern that
