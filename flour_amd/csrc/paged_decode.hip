@@ -20,7 +20,7 @@
 //
 // Inside a piece (bf16/f16 pools, head_dim 128 or 64, block_size a multiple of 16; the
 // figures below are for head_dim 128, and head_dim 64 halves every row: 8-byte lane loads, a
-// 128-byte row per 16 lanes, 4 output dims per lane):
+// 128-byte row per 16 lanes, 16 output dims per lane instead of 32):
 //  * The wave walks its piece chunk by chunk. A chunk is two 16-token MFMA tiles, each one
 //    4 KB (head, 16 slots) pool run of K and of V, read with buffer loads (per-pool resource,
 //    loop-invariant lane offset, per-tile SGPR offset; non-temporal, whole rows per
