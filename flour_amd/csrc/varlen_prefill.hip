@@ -129,8 +129,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // query-tile index ("level"): the cost of an item grows with its tile index (its causal kv
     // range is kv_len - q_len + 128 (qt + 1)), so this is close to longest-first order.
     //  * persistent: one workgroup per CU walks the items that exist (sequences too short for
-    //    a level are left out), item k*G + b on even rounds k and k*G + G-1-b on odd ones
-    //    (a snake over the longest-first list balances the workgroups without shared state);
+    //    a level are left out); the deal over the workgroups is below;
     //  * otherwise: one workgroup per (level, sequence, pair), items past a sequence's last
     //    tile exit at once, and the dispatcher deals the levels over all XCDs.
     const int pairs_per_kv = (n_rep + 1) >> 1;
@@ -182,7 +181,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         }
         return __shfl(incl, 63, 64);  // total
     };
-    int total_items = 0;
+    int total_items = 0, total_base = 0;  // items; (level, sequence) pairs
     if (persistent) {
         for (int i = tid; i <= num_seqs; i += PF_THREADS) sched_cu[i] = cu_seqlens[i];
         for (int i = tid; i < num_seqs; i += PF_THREADS) sched_kv[i] = min(kv_lens[i], kv_cap);
@@ -219,23 +218,31 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         }
         __syncthreads();
         if (w == 0) {
-            // level L (tile qt = NQ-1-L) holds one item per pair of every sequence with more
-            // than qt tiles
-            const int t = wave_scan(NQ, [&](int L) { return npairs * sched_more[NQ - 1 - L]; },
+            // level L (tile qt = NQ-1-L) holds the sequences with more than qt tiles:
+            // sched_cum[L] = sequences on the levels before L
+            const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
                                     [&](int L, int x) { sched_cum[L] = x; }, false);
             if (lane == 0) sched_cum[NQ] = t;
         }
         __syncthreads();
-        total_items = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
+        total_base = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
+        total_items = npairs * total_base;
     }
 
-    // ---- this workgroup's items, decoded once into LDS (one thread per item): the k-th item
-    // is number k*G + b on even k and k*G + G-1-b on odd k of the longest-first list
-    // (persistent), or item b alone (one workgroup per item). An entry holds
+    // ---- this workgroup's items, decoded into LDS (one thread per item). An entry holds
     // {seq, qt, kv head, pair in group, q0, q_len, kv_len, kv tiles}.
+    //  * persistent: the item list is longest-first in two parts: the two-head pairs of every
+    //    level, then (odd n_rep) the one-head pairs, whose items cost about 0.7 of a two-head
+    //    item. Within a part, items go level by level, sequences by decreasing tile count, then
+    //    pairs. The k-th item of workgroup b is number kG + b on even k and kG + G-1-b on odd k
+    //    (a snake over the list balances the workgroups without shared state);
+    //  * otherwise: one workgroup per (level, sequence, pair); items past a sequence's last
+    //    tile exit at once.
     __shared__ __attribute__((aligned(16))) int sched_items[PF_MAX_WG_ITEMS][8];
     __shared__ int sched_nitems;
     {
+        const int half_rep = n_rep >> 1;
+        const int np_full = kv_heads * half_rep, np_lone = kv_heads * (n_rep & 1);
         int n_items = 0;
         if (persistent) {
             const int rounds = total_items / G, rem = total_items - rounds * G;
@@ -245,41 +252,44 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             n_items = 1;
         }
         for (int k = tid; k < n_items; k += PF_THREADS) {
-            int seq, level, hp, q0, ql, kvl;
+            int seq, level, kvh, hj;
             if (persistent) {
                 const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
-                int lo = 0, hi = NQ - 1;  // last level L with sched_cum[L] <= idx
+                const int n_full = np_full * total_base;
+                const bool lone = idx >= n_full;
+                const int ii = lone ? idx - n_full : idx;
+                const int np = lone ? np_lone : np_full;
+                const int key = ii / np;  // (level, sequence) pairs before this item in its part
+                int lo = 0, hi = NQ - 1;  // last level L with sched_cum[L] <= key
                 while (lo < hi) {
                     const int mid = (lo + hi + 1) >> 1;
-                    if (sched_cum[mid] <= idx) lo = mid; else hi = mid - 1;
+                    if (sched_cum[mid] <= key) lo = mid; else hi = mid - 1;
                 }
                 level = lo;
-                const int j = idx - sched_cum[level];
-                const int r = j / npairs;
-                seq = sched_order[r];
-                hp = j - r * npairs;
-                q0 = sched_cu[seq];
-                ql = sched_cu[seq + 1] - q0;
-                kvl = sched_kv[seq];
+                seq = sched_order[key - sched_cum[lo]];
+                const int p = ii - np * key;
+                kvh = lone ? p : p / half_rep;
+                hj = lone ? half_rep : p - kvh * half_rep;
             } else {
                 const int per_rank = num_seqs * npairs;
                 level = wg / per_rank;
                 const int r = wg - level * per_rank;
                 seq = r / npairs;
-                hp = r - seq * npairs;
-                q0 = cu_seqlens[seq];
-                ql = cu_seqlens[seq + 1] - q0;
-                kvl = min(kv_lens[seq], kv_cap);
+                const int hp = r - seq * npairs;
+                kvh = hp / pairs_per_kv;
+                hj = hp - kvh * pairs_per_kv;
             }
+            const int q0 = persistent ? sched_cu[seq] : cu_seqlens[seq];
+            const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - q0;
+            const int kvl = persistent ? sched_kv[seq] : min(kv_lens[seq], kv_cap);
             const int qt = NQ - 1 - level;
-            const int kvh = hp / pairs_per_kv;
             const int row_last = min(qt * PF_QT + PF_QT, ql) - 1;
             const bool ok = qt * PF_QT < ql;  // always true for persistent items
             int* e = sched_items[k];
             e[0] = seq;
             e[1] = qt;
             e[2] = kvh;
-            e[3] = hp - kvh * pairs_per_kv;
+            e[3] = hj;
             e[4] = q0;
             e[5] = ql;
             e[6] = kvl;
