@@ -590,13 +590,22 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         if (kv0 + PF_KT - 1 > wave_min_lim) {
             asm volatile("" ::: "memory");
             const int tl = lim - kv0 - 4 * h2;  // token offset 32mt + 8i + j visible iff <= tl
+            // bit p of vis[mt]: offset 32 mt + p visible. Each score then takes a sign-extended
+            // bit extract and a bit-field select (two VALU, no scalar masks: 32 compares into
+            // scalar masks used to spill scalar registers here).
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
+            for (int mt = 0; mt < 2; mt++) {
+                const int width = min(max(tl + 1 - 32 * mt, 0), 32);
+                const uint32_t vis = width >= 32 ? 0xffffffffu : (1u << width) - 1u;
 #pragma unroll
                 for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        if (32 * mt + 8 * i + j > tl) st[mt][4 * i + j] = -INFINITY;
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe((int)vis, 8 * i + j, 1);
+                        const uint32_t b = __float_as_uint(st[mt][4 * i + j]);
+                        st[mt][4 * i + j] = __uint_as_float((b & keep) | (0xff800000u & ~keep));
+                    }
+            }
         }
         // tile max of the raw scores (scale > 0, so the max commutes with the scaling)
         float tm[2] = {-INFINITY, -INFINITY};
