@@ -152,6 +152,7 @@ EXTRA_SIGNATURES: dict[str, tuple] = {
     "flour_hip_set_prefill_precise_p": (_c_int, [_c_int]),
     "flour_hip_set_decode_workgroups": (_c_int, [_c_int]),
     "flour_hip_set_prefill_persistent": (_c_int, [_c_int]),
+    "flour_hip_set_prefill_dma": (_c_int, [_c_int]),
 }
 
 

@@ -34,6 +34,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "flour_common.h"
@@ -103,26 +104,60 @@ enum { PV_F16 = 0, PV_HILO = 1 };
 
 static constexpr uint32_t PF_OOR = 0x80000000u;  // buffer offset past any pool: loads read 0
 
+// Direct-to-LDS staging (the DMA kernel): three LDS tile buffers; V comes pre-widened from a
+// staging copy of 4 KB pages, each 16 tokens of one kv head as V^T (128 dims x 16 fp16, token
+// sigma16(k) at position k), written by prefill_v_stage_kernel before the attention launch.
+static constexpr int PF_VPAGE_BYTES = 16 * PF_D * 2;
+
+// 64 lanes x 16 bytes from a raw buffer straight into LDS: lane L's bytes come from
+// rsrc.base + soff + voff and land at LDS byte lds + 16 L; lanes past the buffer's size write
+// zeros. Issued from inline asm so that the compiler's wait-count tracking, which knows nothing
+// of these loads, adds no waits for them to the LDS reads; every wait for them is explicit.
+// M0 is written here and nowhere else in the kernel.
+__device__ __forceinline__ void dma_b128(uint32_t voff, __amdgpu_buffer_rsrc_t rsrc, uint32_t lds,
+                                         uint32_t soff) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
+    const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
+                 :: "v"(voff), "s"(rsrc), "s"(l), "s"(so) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 __device__ __forceinline__ int sigma16(int t) {  // swap bits 2 and 3 (token order in V^T rows)
     return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1);
 }
 
-template <typename T, typename TO, int PV, bool BS16>
+template <typename T, typename TO, int PV, bool BS16, bool DMA>
 __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     TO* __restrict__ out, int64_t o_st, int64_t o_sh, const T* __restrict__ q, int64_t q_st,
     int64_t q_sh, const T* __restrict__ k_pool, const T* __restrict__ v_pool,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ block_tables, int max_blocks, int num_seqs, int num_heads,
     int n_rep, int block_size, int64_t num_slots, int n_qt_max, int persistent,
-    float scale_log2) {
+    float scale_log2, const f16_t* __restrict__ v_stage, uint32_t v_stage_bytes) {
+    // DMA: K and V tiles go straight from memory into LDS (K from the pool, V from the staging
+    // copy), three buffers, no staging registers. It needs the persistent schedule and fp16 P.V.
+    static_assert(!DMA || PV == PV_F16, "the DMA kernel runs the fp16 P.V path");
     constexpr int D = PF_D;
     // V^T is staged as fp16 for PV_F16, as the storage type otherwise; K keeps the storage type.
     typedef typename std::conditional<PV == PV_F16, f16_t, T>::type TV;
     // bf16 V is widened to fp16 scaled by 2^8 and each item's output blocks are checked at its
     // end (CHECK_V); a failed check recomputes the item in exact mode.
     constexpr bool CHECK_V = PV == PV_F16 && std::is_same<T, bf16_t>::value;
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][PF_KT * PF_KPITCH];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][PF_D * PF_VPITCH];
+    // LDS tile buffers, each K then V:
+    //  * register staging: K row-major with a 272 B pitch, V^T with a 144 B pitch; two buffers;
+    //  * DMA: K row-major without padding, the 16-byte chunk c of row r stored at chunk
+    //    c ^ (r % 16) (conflict-free fragment reads); V^T as four 4 KB pages (the staging copy's
+    //    layout), or in exact mode the register-staged V^T with a 144 B pitch; three buffers.
+    constexpr int NBUF = DMA ? 3 : 2;
+    constexpr int K_ELEMS = DMA ? PF_KT * PF_D : PF_KT * PF_KPITCH;
+    constexpr int TILE_ELEMS = K_ELEMS + PF_D * PF_VPITCH;
+    static_assert(!DMA || 8 * 32 * PF_OPITCH <= TILE_ELEMS, "output staging fits one buffer");
+    __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF * TILE_ELEMS];
+    auto kb_ptr = [&](int b) { return &tiles[b * TILE_ELEMS]; };
+    auto vb_ptr = [&](int b) { return &tiles[b * TILE_ELEMS + K_ELEMS]; };
     __shared__ __attribute__((aligned(8))) uint8_t redo_flag[PF_WAVES];  // per wave, item end
 
     // ---- work items: (query tile, sequence, pair of query heads), ordered by decreasing
@@ -150,6 +185,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     __shared__ int sched_cum[PF_MAX_LEVELS + 2];   // [L]: items before level L
     __shared__ int sched_cu[PF_MAX_SEQS + 1];      // cu_seqlens
     __shared__ int sched_kv[PF_MAX_SEQS];          // clamped kv lengths
+    // DMA: first staging-copy page of each sequence (4 pages per 64-token kv tile)
+    __shared__ int sched_vpage[DMA ? PF_MAX_SEQS : 1];
     // query tiles of a sequence; one with kv_len < q_len still has its tiles, whose items
     // attend nothing and write zero rows (as the generic path and the oracle do)
     auto seq_tiles = [&](int sq) {
@@ -223,6 +260,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
                                     [&](int L, int x) { sched_cum[L] = x; }, false);
             if (lane == 0) sched_cum[NQ] = t;
+        }
+        if (DMA && w == 1) {
+            wave_scan(num_seqs,
+                      [&](int sq) { return 4 * ((max(sched_kv[sq], 0) + PF_KT - 1) / PF_KT); },
+                      [&](int sq, int x) { sched_vpage[sq] = x; }, false);
         }
         __syncthreads();
         total_base = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
@@ -304,7 +346,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 
     // A work item (all fields workgroup-uniform); valid == 0 past the end of the list.
     struct Item {
-        int valid, seq, qt, kvh, hj, q0, ql, kv_len, n_kt, last_page;
+        int valid, seq, qt, kvh, hj, q0, ql, kv_len, n_kt, last_page, vpage;
     };
     auto uni = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
     auto fetch = [&](int k) __attribute__((always_inline)) {
@@ -323,6 +365,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             it.n_kt = uni(b.w);
             // (page 0 for an empty sequence: its loads are all masked, its table row exists)
             it.last_page = it.kv_len > 0 ? (BS16 ? (it.kv_len - 1) >> 4 : (it.kv_len - 1) / block_size) : 0;
+            if constexpr (DMA) it.vpage = uni(sched_vpage[it.seq]);
         }
         return it;
     };
@@ -343,11 +386,25 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     const uint32_t k_lane = (uint32_t)((k_row & 15) * D + k_col) * (uint32_t)sizeof(T);
     const uint32_t v_lane = (uint32_t)((2 * v_tp & 15) * D + 8 * v_dg) * (uint32_t)sizeof(T);
     const bool v_g1 = (v_tp >> 3) & 1, v_g2 = (v_tp >> 4) & 1;
+    // DMA: wave w fills K rows 8w .. 8w+7 of the tile (all in group w / 2) with two 1 KB loads;
+    // lane (r4, c) = (lane / 16, lane % 16) of load i reads row 8w + 4i + r4 (row r of the
+    // group), 16-byte chunk c ^ r, which lands at chunk c of that row. For V, wave w copies half
+    // w % 2 of page w / 2 of the tile (two 1 KB loads).
+    uint32_t kdma_lane[2] = {0u, 0u};
+    if constexpr (DMA) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int r = 8 * (w & 1) + 4 * i + (lane >> 4);
+            kdma_lane[i] = (uint32_t)(r * (int)ROW_BYTES + ((lane & 15) ^ r) * 16);
+        }
+    }
+    const __amdgpu_buffer_rsrc_t vst_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)v_stage, (short)0, (int)v_stage_bytes, BUF_DWORD3);
 
     // ---- load context: the item whose K / V tiles are being fetched
     __amdgpu_buffer_rsrc_t k_rsrc, v_rsrc;
     const int32_t* bt = block_tables;
-    int kv_len = 0, last_page = 0, n_kt = 0;
+    int kv_len = 0, last_page = 0, n_kt = 0, ld_vpage = 0, ld_kvh = 0;
     auto set_load = [&](const Item& it) {
         k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(k_pool + (int64_t)it.kvh * num_slots * D), (short)0, (int)head_bytes, BUF_DWORD3);
@@ -357,6 +414,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         kv_len = it.kv_len;
         last_page = it.last_page;
         n_kt = it.n_kt;
+        ld_vpage = it.vpage;
+        ld_kvh = it.kvh;
     };
     // Block ids reach the tile loads through a window of the block table held in VGPRs (lane
     // i: entry wbase + i in win_cur, wbase + 64 + i in win_next), refilled 64 entries ahead
@@ -411,6 +470,15 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
     // Branch-free tile loads into (kd, vd): tokens past kv_len (or a tile past the last) get an
     // out-of-range offset and read zeros.
+    auto gload_v = [&](int kt, const int* pb, bool valid, u32x4* vd) {
+        const int lim_rel = (valid ? kv_len : 0) - kt * PF_KT;  // tile tokens t < lim_rel exist
+        const int b01 = v_g1 ? pb[1] : pb[0], b23 = v_g1 ? pb[3] : pb[2];
+        const uint32_t vb = (uint32_t)(v_g2 ? b23 : b01) + v_lane;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            vd[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                v_rsrc, 2 * v_tp + j < lim_rel ? vb + j * ROW_BYTES : PF_OOR, 0, BUF_NT);
+    };
     auto gload = [&](int kt, const int* pb, bool valid, u32x4* kd, u32x4* vd) {
         const int lim_rel = (valid ? kv_len : 0) - kt * PF_KT;  // tile tokens t < lim_rel exist
 #pragma unroll
@@ -419,18 +487,32 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             kd[i] = __builtin_amdgcn_raw_buffer_load_b128(
                 k_rsrc, k_row + 32 * i < lim_rel ? o : PF_OOR, 0, 0);
         }
-        const int b01 = v_g1 ? pb[1] : pb[0], b23 = v_g1 ? pb[3] : pb[2];
-        const uint32_t vb = (uint32_t)(v_g2 ? b23 : b01) + v_lane;
+        gload_v(kt, pb, valid, vd);
+    };
+    // DMA: tile kt's K into buffer b (rows past kv_len read zeros) and, outside exact mode, its
+    // V pages from the staging copy.
+    auto dma_tile = [&](auto ex, int kt, const int* pb, int b) __attribute__((always_inline)) {
+        const int lim_rel = kv_len - kt * PF_KT;
+        const int g = w >> 1;  // this wave's 16-token group
+        const int pgb = g == 0 ? pb[0] : g == 1 ? pb[1] : g == 2 ? pb[2] : pb[3];
+        const uint32_t kdst = lds_byte_addr(kb_ptr(b)) + (uint32_t)w * 2048u;
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-            vd[j] = __builtin_amdgcn_raw_buffer_load_b128(
-                v_rsrc, 2 * v_tp + j < lim_rel ? vb + j * ROW_BYTES : PF_OOR, 0, BUF_NT);
+        for (int i = 0; i < 2; i++) {
+            const int row = 8 * w + 4 * i + (lane >> 4);
+            dma_b128(row < lim_rel ? kdma_lane[i] : PF_OOR, k_rsrc, kdst + 1024u * i, (uint32_t)pgb);
+        }
+        if constexpr (!decltype(ex)::value) {
+            const uint32_t vdst = lds_byte_addr(vb_ptr(b)) + (uint32_t)w * 2048u;
+            const uint32_t vso =
+                (uint32_t)((ld_vpage + 4 * kt + g) * kv_heads + ld_kvh) * (uint32_t)PF_VPAGE_BYTES +
+                (uint32_t)(w & 1) * 2048u;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                dma_b128((uint32_t)lane * 16u + 1024u * i, vst_rsrc, vdst + 1024u * i, vso);
+        }
     };
     // `ex` true: exact mode, V is stored as bf16 without widening
-    auto lds_store = [&](auto ex, int buf, u32x4* kd, u32x4* vd) {
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            *reinterpret_cast<u32x4*>(&Ks[buf][(k_row + 32 * i) * PF_KPITCH + k_col]) = kd[i];
+    auto lds_store_v = [&](auto ex, int buf, u32x4* vd) {
         if constexpr (CHECK_V && !decltype(ex)::value) {
             // widen bf16 V to fp16 as v * 2^8 (exact for 2^-25 <= |v| <= 255 and 0)
 #pragma unroll
@@ -445,8 +527,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         for (int e = 0; e < 8; e++) {
             const int wd = e >> 1;
             const uint32_t pr = (e & 1) ? perm_hi16(vd[0][wd], vd[1][wd]) : perm_lo16(vd[0][wd], vd[1][wd]);
-            *reinterpret_cast<uint32_t*>(&Vt[buf][(8 * v_dg + e) * PF_VPITCH + col]) = pr;
+            *reinterpret_cast<uint32_t*>(&vb_ptr(buf)[(8 * v_dg + e) * PF_VPITCH + col]) = pr;
         }
+    };
+    auto lds_store = [&](auto ex, int buf, u32x4* kd, u32x4* vd) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            *reinterpret_cast<u32x4*>(&kb_ptr(buf)[(k_row + 32 * i) * PF_KPITCH + k_col]) = kd[i];
+        lds_store_v(ex, buf, vd);
     };
 
     // ---- per-item compute state (the item whose tile the workgroup is computing)
@@ -489,7 +577,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             for (int y = 0; y < 16; y++) o[x][y] = 0.0f;
     };
     // ---- epilogue: lane (h2, q) holds dims 32 mt2 + 8 i + 4 h2 + j of query row wr0 + q
-    auto store_output = [&]() __attribute__((always_inline)) {
+    auto store_output = [&](int sbuf) __attribute__((always_inline)) {
         const float l = lsum + wave_shfl_xor(lsum, 32);
         if (wave_active) {
             // 0: an item that attends nothing; out_scale undoes the widening scale of V
@@ -507,11 +595,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                                       o[mt2][4 * i + 2] * inv, o[mt2][4 * i + 3] * inv};
                 }
             } else {
-                // 16-bit output goes through LDS (the second K / V buffer, idle until the next
-                // item's first tile is staged, which follows a barrier) in two 64-dim halves, so
-                // that each store writes whole 128 B row segments: lane (r, c) = (lane / 8,
-                // lane % 8) stores dims 8c .. 8c + 7 of rows r, r + 8, r + 16, r + 24.
-                uint16_t* stg = (w < 4 ? &Ks[1][0] : &Vt[1][0]) + (w & 3) * (32 * PF_OPITCH);
+                // 16-bit output goes through LDS (tile buffer sbuf, idle until a barrier that
+                // comes before its next fill) in two 64-dim halves, so that each store writes
+                // whole 128 B row segments: lane (r, c) = (lane / 8, lane % 8) stores dims
+                // 8c .. 8c + 7 of rows r, r + 8, r + 16, r + 24.
+                uint16_t* stg = DMA ? kb_ptr(sbuf) + w * (32 * PF_OPITCH)
+                                    : (w < 4 ? kb_ptr(sbuf) : vb_ptr(sbuf)) + (w & 3) * (32 * PF_OPITCH);
                 const int rr = lane >> 3, cc = lane & 7;
                 TO* ob = out + (int64_t)(q0 + wr0) * o_st + (int64_t)head * o_sh + 8 * cc;
 #pragma unroll
@@ -548,9 +637,16 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // read four products ahead. `fill` is work independent of the scores (the staging of the
     // next tile) that the products are interleaved with.
     auto qk = [&](int kbuf, auto&& fill) __attribute__((always_inline)) {
-        const uint16_t* kr = &Ks[kbuf][ql32 * PF_KPITCH + 8 * h2];
+        const uint16_t* kr = DMA ? kb_ptr(kbuf) + ql32 * PF_D : kb_ptr(kbuf) + ql32 * PF_KPITCH + 8 * h2;
         auto frag = [&](int i) {  // product i: half i & 1, dims 16 (i >> 1) .. of the K rows
-            return *reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * PF_KPITCH + 16 * (i >> 1));
+            if constexpr (DMA) {
+                // 16-byte chunk 2 (i >> 1) + h2 of row ql32 + 32 (i & 1), stored at chunk
+                // (2 (i >> 1) + h2) ^ (ql32 % 16)
+                return *reinterpret_cast<const u32x4*>(
+                    kr + (i & 1) * 32 * PF_D + 8 * ((2 * (i >> 1) + h2) ^ (ql32 & 15)));
+            } else {
+                return *reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * PF_KPITCH + 16 * (i >> 1));
+            }
         };
         u32x4 fr[16];
 #pragma unroll
@@ -652,11 +748,16 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         // Issue order, pinned with scheduling fences: the V reads and weights of step 0, then
         // each product of step kk2 followed by one V read and a quarter of the weights of
         // step kk2 + 1.
-        const uint16_t* vr = &Vt[vbuf][ql32 * PF_VPITCH + 8 * h2];
+        // V^T fragment (dims 32 mt2 + ql32, tokens 8 h2 .. of group kk2): register staging keeps
+        // V^T rows with a 144 B pitch; the DMA path has four 4 KB pages (128 dims x 16 tokens)
+        const uint16_t* vr = DMA ? vb_ptr(vbuf) + ql32 * 16 + 8 * h2 : vb_ptr(vbuf) + ql32 * PF_VPITCH + 8 * h2;
+        auto vfrag = [&](int mt2, int kk2) {
+            return *reinterpret_cast<const u32x4*>(
+                DMA ? vr + kk2 * (16 * PF_D) + mt2 * 512 : vr + 32 * mt2 * PF_VPITCH + 16 * kk2);
+        };
         u32x4 vf[2][4];
 #pragma unroll
-        for (int mt2 = 0; mt2 < 4; mt2++)
-            vf[0][mt2] = *reinterpret_cast<const u32x4*>(vr + 32 * mt2 * PF_VPITCH);
+        for (int mt2 = 0; mt2 < 4; mt2++) vf[0][mt2] = vfrag(mt2, 0);
 #pragma unroll
         for (int x = 0; x < 4; x++) weight(0, x);
         __builtin_amdgcn_sched_barrier(0);
@@ -669,8 +770,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 if constexpr (PV == PV_HILO)
                     o[mt2] = mfma32x32x16<TV>(vf[kk2 & 1][mt2], pb_lo[kk2], o[mt2]);
                 if (kk2 < 3) {
-                    vf[(kk2 + 1) & 1][mt2] = *reinterpret_cast<const u32x4*>(
-                        vr + 32 * mt2 * PF_VPITCH + 16 * (kk2 + 1));
+                    vf[(kk2 + 1) & 1][mt2] = vfrag(mt2, kk2 + 1);
                     weight(kk2 + 1, mt2);
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -685,7 +785,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         softmax_max(kt, 0.0f);
         const float nm = -m;
         float psum = 0.0f;
-        const uint16_t* vr = &Vt[vbuf][ql32 * PF_VPITCH + 8 * h2];
+        const uint16_t* vr = vb_ptr(vbuf) + ql32 * PF_VPITCH + 8 * h2;
 #pragma unroll
         for (int kk2 = 0; kk2 < 4; kk2++) {
             const int mt = kk2 >> 1, y0 = 8 * (kk2 & 1);
@@ -717,16 +817,31 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     if (n_items == 0) return;
     u32x4 ka[2], va[2], kb[2], vb[2];
     int pb0[4], pb1[4], pb2[4];
+    // DMA: the buffers rotate over the tiles of consecutive items; buf0 is the buffer of the
+    // first tile of the item in the load context
+    int buf0 = 0;
+    auto next_buf = [](int b) { return b == NBUF - 1 ? 0 : b + 1; };
+    auto prev_buf = [](int b) { return b == 0 ? NBUF - 1 : b - 1; };
     // the first tiles of the item in the load context: tiles 0 and 1 in flight, page ids of
     // tile 2 ready, the block-table windows at the start (win_cur must hold entries 0..63)
-    auto start_tiles = [&]() __attribute__((always_inline)) {
+    auto start_tiles = [&](auto ex) __attribute__((always_inline)) {
         wbase = 0;
         ld_ok = false;
         win_next = load_window(bt, 64, last_page + 1);
         page_bases(0, pb0);
-        gload(0, pb0, true, ka, va);
+        if constexpr (DMA) {
+            if (0 < n_kt) dma_tile(ex, 0, pb0, buf0);
+            if constexpr (decltype(ex)::value) gload_v(0, pb0, true, va);
+        } else {
+            gload(0, pb0, true, ka, va);
+        }
         page_bases(min(1, n_kt - 1), pb1);
-        gload(1, pb1, 1 < n_kt, kb, vb);
+        if constexpr (DMA) {
+            if (1 < n_kt) dma_tile(ex, 1, pb1, next_buf(buf0));
+            if constexpr (decltype(ex)::value) gload_v(1, pb1, 1 < n_kt, vb);
+        } else {
+            gload(1, pb1, 1 < n_kt, kb, vb);
+        }
         page_bases(min(2, n_kt - 1), pb2);
     };
     auto prologue = [&](const Item& it, const Item& after) __attribute__((always_inline)) {
@@ -736,7 +851,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         if (after.valid)  // first window of the item after this one
             win_pre = load_window(block_tables + (int64_t)after.seq * max_blocks, 0,
                                   after.last_page + 1);
-        start_tiles();
+        start_tiles(std::false_type{});
     };
     // Item-end check of the fp16 path (CHECK_V): true if this wave's output block is not finite
     // or its largest |output| is below PF_MIN_TRUSTED (both in the 2^8-scaled accumulator:
@@ -759,46 +874,100 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     prologue(ci, fetch(1));
     set_compute(ci);
     for (int k = 0;;) {
-        // step kt: refill `nx` with tile kt + 2, compute tile kt, store tile kt + 1 (in `st1`).
-        // `ex`: exact mode. On the fp16 path the last step records this wave's item-end check
-        // before its barrier, which publishes it.
-        auto step = [&](auto ex, int kt, u32x4* knx, u32x4* vnx, u32x4* kst1,
-                        u32x4* vst1) __attribute__((always_inline)) {
+        // compute tile kt from LDS buffer bc; `ex`: exact mode. On the fp16 path the last step
+        // records this wave's item-end check before its barrier, which publishes it.
+        auto compute = [&](auto ex, int kt, int bc) __attribute__((always_inline)) {
             constexpr bool EX = decltype(ex)::value;
-            gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
-            page_bases(min(kt + 3, n_kt - 1), pb0);
             if (visible(kt)) {
-                qk(kt & 1, [] {});
+                qk(bc, [] {});
                 if constexpr (EX)
-                    sm_pv_exact(kt, kt & 1);
+                    sm_pv_exact(kt, bc);
                 else
-                    sm_pv(kt, kt & 1);
+                    sm_pv(kt, bc);
             }
             if constexpr (CHECK_V && !EX) {
                 if (kt == n_kt - 1) redo_flag[w] = block_untrusted() ? 1 : 0;
             }
-            lds_store(ex, (kt + 1) & 1, kst1, vst1);
+        };
+        auto rotate_pages = [&]() __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {  // pb2 <- tile kt + 3
                 const int x = pb2[i];
                 pb2[i] = pb0[i];
                 pb0[i] = x;
             }
+        };
+        // register staging, step kt: refill `nx` with tile kt + 2, compute tile kt, store tile
+        // kt + 1 (in `st1`).
+        auto step = [&](auto ex, int kt, u32x4* knx, u32x4* vnx, u32x4* kst1,
+                        u32x4* vst1) __attribute__((always_inline)) {
+            gload(kt + 2, pb2, kt + 2 < n_kt, knx, vnx);
+            page_bases(min(kt + 3, n_kt - 1), pb0);
+            compute(ex, kt, kt & 1);
+            lds_store(ex, (kt + 1) & 1, kst1, vst1);
+            rotate_pages();
+            __syncthreads();
+        };
+        // DMA, step kt with tile kt in buffer bc: tile kt + 2 goes to the buffer of tile kt - 1
+        // (free since the last barrier), then tile kt is computed and the wait for tile kt + 1
+        // (the oldest loads in flight) precedes the barrier. The page ids of tile kt + 3 come
+        // first: a block-table window move waits for every load in flight, and at that point
+        // the newest are tile kt + 1's, due before the barrier anyway. In exact mode V goes
+        // through registers (tile kt + 2 loaded, tile kt + 1 written to LDS).
+        auto step_dma = [&](auto ex, int kt, int bc, u32x4* vnx, u32x4* vst1) __attribute__((always_inline)) {
+            constexpr bool EX = decltype(ex)::value;
+            page_bases(min(kt + 3, n_kt - 1), pb0);
+            const bool more = kt + 2 < n_kt;
+            if (more) dma_tile(ex, kt + 2, pb2, prev_buf(bc));
+            if constexpr (EX) gload_v(kt + 2, pb2, more, vnx);
+            compute(ex, kt, bc);
+            if constexpr (EX) lds_store_v(ex, next_buf(bc), vst1);
+            rotate_pages();
+            if constexpr (EX) {
+                asm volatile("s_waitcnt vmcnt(2)" ::: "memory");  // all but tile kt + 2's V
+            } else if (more) {
+                asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // all but tile kt + 2's
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
             __syncthreads();
         };
         // all tiles of the current item, from tiles 0 and 1 in flight (start_tiles)
         auto run_tiles = [&](auto ex) __attribute__((always_inline)) {
+            constexpr bool EX = decltype(ex)::value;
             reset_state();
             // Q must have landed before the loop (its loads precede the tile loads, so this
             // waits for them alone); otherwise the compiler sinks the Q loads past the first
             // barrier and keeps a conservative wait for them inside the loop
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) asm volatile("" ::"v"(qb[kk]));
-            lds_store(ex, 0, ka, va);
-            __syncthreads();
-            for (int kt = 0; kt < n_kt; kt += 2) {
-                step(ex, kt, ka, va, kb, vb);
-                if (kt + 1 < n_kt) step(ex, kt + 1, kb, vb, ka, va);
+            if constexpr (DMA) {
+                if constexpr (EX) {
+                    lds_store_v(ex, buf0, va);
+                    asm volatile("s_waitcnt vmcnt(2)" ::: "memory");  // all but tile 1's V
+                } else if (1 < n_kt) {
+                    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // all but tile 1's
+                } else {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                }
+                __syncthreads();
+                int bc = buf0;
+                for (int kt = 0; kt < n_kt; kt += 2) {
+                    step_dma(ex, kt, bc, va, vb);
+                    bc = next_buf(bc);
+                    if (kt + 1 < n_kt) {
+                        step_dma(ex, kt + 1, bc, vb, va);
+                        bc = next_buf(bc);
+                    }
+                }
+                buf0 = bc;
+            } else {
+                lds_store(ex, 0, ka, va);
+                __syncthreads();
+                for (int kt = 0; kt < n_kt; kt += 2) {
+                    step(ex, kt, ka, va, kb, vb);
+                    if (kt + 1 < n_kt) step(ex, kt + 1, kb, vb, ka, va);
+                }
             }
         };
         run_tiles(std::false_type{});
@@ -811,20 +980,110 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
             if (redo) {  // the whole item again in exact mode (every wave, uniform branch)
                 win_cur = load_window(bt, 0, last_page + 1);
-                start_tiles();
+                start_tiles(std::true_type{});
                 run_tiles(std::true_type{});
                 out_scale = 1.0f;
             }
         }
+        // output staging: register staging's second buffer (both are idle here), or the DMA
+        // buffer of the item's last tile (the next item's first tiles go to the two after it)
+        const int sbuf = DMA ? prev_buf(buf0) : 1;
         const Item nx = fetch(++k);
         if (nx.valid) prologue(nx, fetch(k + 1));
-        store_output();
+        store_output(sbuf);
         if (!nx.valid) break;
         set_compute(nx);
     }
 }
 
+// Staging copy of V for the DMA kernel: every 16-token page of each sequence's kv range,
+// rounded up to whole 64-token tiles, as V^T in fp16 (128 dims x 16 tokens, token sigma16(k) at
+// position k; bf16 values times 2^8 by the same conversion as the register-staged path), tokens
+// past kv_len zero. Page p of sequence s and kv head h is at ((vpage(s) + p) * kv_heads + h)
+// * 4 KB, vpage(s) = the sum over earlier sequences of 4 * ceil(kv_len / 64), kv lengths clamped
+// to the block table. One 512-thread workgroup per 8 pages of one kv head.
+static constexpr int PF_STAGE_PAGES = 8;
+template <typename T>
+__global__ __launch_bounds__(512) void prefill_v_stage_kernel(
+    f16_t* __restrict__ ws, const T* __restrict__ v_pool, const int32_t* __restrict__ kv_lens,
+    const int32_t* __restrict__ block_tables, int max_blocks, int kv_heads, int block_size,
+    int64_t num_slots, int chunks_per_seq) {
+    __shared__ __attribute__((aligned(16))) uint16_t tp[PF_STAGE_PAGES][PF_D * 16];
+    __shared__ int s_base;
+    const int seq = blockIdx.x / chunks_per_seq;
+    const int p0 = (blockIdx.x - seq * chunks_per_seq) * PF_STAGE_PAGES;
+    const int kvh = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int kv_cap = max_blocks * block_size;
+    auto pages_of = [&](int sq) {
+        return 4 * ((max(min(kv_lens[sq], kv_cap), 0) + PF_KT - 1) / PF_KT);
+    };
+    const int kvl = max(min(kv_lens[seq], kv_cap), 0);
+    const int n_pages = pages_of(seq);
+    if (p0 >= n_pages) return;
+    if (tid < 64) {  // this sequence's first page
+        int acc = 0;
+        for (int s2 = tid; s2 < seq; s2 += 64) acc += pages_of(s2);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (tid == 0) s_base = acc;
+    }
+    // thread (i, m, c) = (tid / 64, (tid / 16) % 4, tid % 16): page p0 + i, tokens 4m .. 4m + 3,
+    // dims 8c .. 8c + 7 (a page lies in one block: block sizes are multiples of 16). Tokens
+    // 4m + j sit at positions sigma16(4m) + j, so each dim's four values are one 8-byte store.
+    const int i = tid >> 6, m = (tid >> 4) & 3, c = tid & 15;
+    const int p = p0 + i;
+    const int tok0 = 16 * p + 4 * m;
+    u32x4 v[4] = {};
+    if (p < n_pages && tok0 < kvl) {
+        const int lb = (16 * p) / block_size;
+        const int max_phys = (int)(num_slots / block_size - 1);
+        const int phys = min(max(block_tables[(int64_t)seq * max_blocks + lb], 0), max_phys);
+        const T* src = v_pool + ((int64_t)kvh * num_slots + (int64_t)phys * block_size +
+                                 (tok0 - lb * block_size)) * PF_D + 8 * c;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (tok0 + j < kvl) v[j] = *reinterpret_cast<const u32x4*>(src + j * PF_D);
+    }
+    if constexpr (std::is_same<T, bf16_t>::value) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+                v[j][x] = pack2<f16_t>(lo_f32<bf16_t>(v[j][x]) * PF_V_SCALE,
+                                       hi_f32<bf16_t>(v[j][x]) * PF_V_SCALE);
+    }
+    const int pos = sigma16(4 * m);
+#pragma unroll
+    for (int x = 0; x < 4; x++) {
+        // dims 8c + 2x (low halves) and 8c + 2x + 1 (high halves) of tokens 4m .. 4m + 3
+        *reinterpret_cast<u32x2*>(&tp[i][(8 * c + 2 * x) * 16 + pos]) =
+            u32x2{perm_lo16(v[0][x], v[1][x]), perm_lo16(v[2][x], v[3][x])};
+        *reinterpret_cast<u32x2*>(&tp[i][(8 * c + 2 * x + 1) * 16 + pos]) =
+            u32x2{perm_hi16(v[0][x], v[1][x]), perm_hi16(v[2][x], v[3][x])};
+    }
+    __syncthreads();
+    // thread (i, d) = (tid / 64, tid % 64): dims 2d, 2d + 1 of page p0 + i, 64 contiguous bytes
+    const int d2 = 2 * (tid & 63);
+    if (p < n_pages) {
+        f16_t* dst = ws + ((int64_t)(s_base + p) * kv_heads + kvh) * (PF_D * 16) + d2 * 16;
+        const u32x4* src = reinterpret_cast<const u32x4*>(&tp[i][d2 * 16]);
+#pragma unroll
+        for (int x = 0; x < 4; x++) reinterpret_cast<u32x4*>(dst)[x] = src[x];
+    }
+}
+
 static int g_prefill_persistent = 1;  // a tuning / test switch
+// Direct-to-LDS staging: 0 never, 1 for long prompts (PF_DMA_MIN_MEAN_Q), 2 whenever the
+// persistent fp16 P.V path runs; a tuning / test switch.
+static int g_prefill_dma = 1;
+// The V staging copy is paid once per kv tile; the saving comes with every query tile that reads
+// it. Measured on Llama-3-8B heads (32 q / 8 kv, causal, no prefix), DMA over register staging:
+// +2% at 16 x 1,024 rows, +6% at 8 x 2,048, +7% at 4 x 4,096 and 1 x 16,384; a ragged batch
+// of 8 x 256-2,048 rows (mean ~1,150) breaks even.
+static constexpr int PF_DMA_MIN_MEAN_Q = 1536;
+// Largest staging copy the DMA path takes; beyond it the launch uses register staging.
+static constexpr int64_t PF_STAGE_MAX_BYTES = int64_t(1) << 30;
 
 static int device_cus() {
     static int cached[64] = {0};
@@ -840,13 +1099,47 @@ static int device_cus() {
     return cached[dev];
 }
 
+// Stream-ordered allocation of the V staging copy from the device's default memory pool, whose
+// release threshold is raised once so that freed blocks stay cached for the next call. False
+// (and nothing allocated) when the stream is being captured into a graph, the device has no
+// memory pools or the allocation fails: the caller then takes the register-staged path.
+static bool stage_alloc(void** p, size_t bytes, hipStream_t stream) {
+    static std::once_flag once[64];
+    static int pools_ok[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+        return false;
+    std::call_once(once[dev], [dev] {
+        int supported = 0;
+        hipMemPool_t pool = nullptr;
+        if (hipDeviceGetAttribute(&supported, hipDeviceAttributeMemoryPoolsSupported, dev) !=
+                hipSuccess ||
+            !supported || hipDeviceGetDefaultMemPool(&pool, dev) != hipSuccess) {
+            pools_ok[dev] = 0;
+            return;
+        }
+        uint64_t keep = UINT64_MAX;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        pools_ok[dev] = 1;
+    });
+    if (!pools_ok[dev]) return false;
+    if (hipMallocAsync(p, bytes, stream) != hipSuccess) {
+        (void)hipGetLastError();  // clear the failed call's error state
+        *p = nullptr;
+        return false;
+    }
+    return true;
+}
+
 template <typename T, typename TO, int PV>
 static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void* q,
                                int64_t q_st, int64_t q_sh, const void* k_pool, const void* v_pool,
                                const int32_t* cu, const int32_t* kv_lens, const int32_t* bt,
-                               int max_blocks, int num_seqs, int max_seqlen_q, int num_heads,
-                               int n_rep, int block_size, int64_t num_slots, float scale,
-                               hipStream_t stream) {
+                               int max_blocks, int num_seqs, int max_seqlen_q, int total_q,
+                               int num_heads, int n_rep, int block_size, int64_t num_slots,
+                               float scale, hipStream_t stream) {
     const int64_t n_qt = (max_seqlen_q + PF_QT - 1) / PF_QT;
     const int64_t items = n_qt * num_seqs * (num_heads / n_rep) * ((n_rep + 1) / 2);
     const int64_t cus = device_cus();
@@ -858,13 +1151,45 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
         return FLOUR_ERR_UNSUPPORTED;
     }
     if (grid == 0) return FLOUR_OK;
-    auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true>
-                                 : varlen_prefill_mfma_kernel<T, TO, PV, false>;
+    if constexpr (PV == PV_F16) {
+        // DMA path: the V staging copy lives in a stream-ordered allocation (no host sync;
+        // calls on other streams get their own), then two launches.
+        const int kv_heads = num_heads / n_rep;
+        const int64_t pages_per_seq = 4 * (((int64_t)max_blocks * block_size + PF_KT - 1) / PF_KT);
+        const int64_t ws_bytes = (int64_t)num_seqs * pages_per_seq * kv_heads * PF_VPAGE_BYTES;
+        const bool want = g_prefill_dma == 2 ||
+                          (g_prefill_dma == 1 && total_q >= (int64_t)PF_DMA_MIN_MEAN_Q * num_seqs);
+        void* ws = nullptr;
+        if (want && persistent && ws_bytes <= PF_STAGE_MAX_BYTES &&
+            stage_alloc(&ws, (size_t)ws_bytes, stream)) {
+            const int64_t chunks = (pages_per_seq + PF_STAGE_PAGES - 1) / PF_STAGE_PAGES;
+            prefill_v_stage_kernel<T><<<dim3((unsigned)(num_seqs * chunks), (unsigned)kv_heads),
+                                        dim3(512), 0, stream>>>(
+                static_cast<f16_t*>(ws), static_cast<const T*>(v_pool), kv_lens, bt, max_blocks,
+                kv_heads, block_size, num_slots, (int)chunks);
+            int rc = check_hip(hipGetLastError(), "varlen_prefill V staging launch");
+            if (rc == FLOUR_OK) {
+                auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, true>
+                                             : varlen_prefill_mfma_kernel<T, TO, PV, false, true>;
+                kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
+                    static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
+                    static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt,
+                    max_blocks, num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt,
+                    (int)persistent, scale * PF_LOG2E, static_cast<const f16_t*>(ws),
+                    (uint32_t)ws_bytes);
+                rc = check_hip(hipGetLastError(), "varlen_prefill launch");
+            }
+            const int frc = check_hip(hipFreeAsync(ws, stream), "varlen_prefill staging free");
+            return rc != FLOUR_OK ? rc : frc;
+        }
+    }
+    auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, false>
+                                 : varlen_prefill_mfma_kernel<T, TO, PV, false, false>;
     kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
         static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
         static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt, max_blocks,
         num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt, (int)persistent,
-        scale * PF_LOG2E);
+        scale * PF_LOG2E, nullptr, 0u);
     return check_hip(hipGetLastError(), "varlen_prefill launch");
 }
 
@@ -877,6 +1202,17 @@ using namespace flour;
 
 extern "C" int flour_hip_set_prefill_persistent(int on) {
     g_prefill_persistent = on ? 1 : 0;
+    return FLOUR_OK;
+}
+
+// 0: register staging only; 1: direct-to-LDS staging for long prompts (the default);
+// 2: direct-to-LDS staging whenever the persistent fp16 P.V path runs.
+extern "C" int flour_hip_set_prefill_dma(int mode) {
+    if (mode < 0 || mode > 2) {
+        set_error("set_prefill_dma: mode %d is not 0, 1 or 2", mode);
+        return FLOUR_ERR_INVALID_ARGUMENT;
+    }
+    g_prefill_dma = mode;
     return FLOUR_OK;
 }
 
@@ -940,18 +1276,14 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
     }
 #define FLOUR_PF(T, TO)                                                                          \
     return g_prefill_pv_mode == PV_HILO                                                          \
-               ? launch_prefill_mfma<T, TO, PV_HILO>(out, o_stride_tok, o_stride_head, q,        \
-                                                     q_stride_tok, q_stride_head, k_pool, v_pool, \
-                                                     cu_seqlens_q, kv_lens, block_tables,        \
-                                                     max_blocks_per_seq, num_seqs, max_seqlen_q, \
-                                                     num_heads, n_rep, block_size, num_slots,    \
-                                                     scale, s)                                   \
-               : launch_prefill_mfma<T, TO, PV_F16>(out, o_stride_tok, o_stride_head, q,         \
-                                                    q_stride_tok, q_stride_head, k_pool, v_pool,  \
-                                                    cu_seqlens_q, kv_lens, block_tables,         \
-                                                    max_blocks_per_seq, num_seqs, max_seqlen_q,  \
-                                                    num_heads, n_rep, block_size, num_slots,     \
-                                                    scale, s)
+               ? launch_prefill_mfma<T, TO, PV_HILO>(                                            \
+                     out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
+                     v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
+                     max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale, s)   \
+               : launch_prefill_mfma<T, TO, PV_F16>(                                             \
+                     out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
+                     v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
+                     max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale, s)
     if (dtype == FLOUR_DTYPE_BF16) {
         if (out_dtype == FLOUR_DTYPE_F32) FLOUR_PF(bf16_t, float);
         if (out_dtype == FLOUR_DTYPE_BF16) FLOUR_PF(bf16_t, bf16_t);

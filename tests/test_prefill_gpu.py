@@ -353,6 +353,59 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
+@pytest.mark.parametrize("case", ["varlen", "prefix", "bs64", "f16", "v_huge", "crossings"])
+def test_prefill_dma_staging_matches_register_staging(device, case):
+    """Direct-to-LDS staging (K rows from the pool and V pages from a transposed fp16 staging
+    copy, both by buffer loads into LDS) gives bit-identical output to register staging:
+    ragged lengths with empty sequences and kv_len < q_len, prefix-cached kv, 64-token blocks,
+    fp16 pools, V outside the fp16 range (the exact-mode redo) and tiles straddling blocks."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(17)
+    H, G, bs, prefix, dt = 8, 2, 16, 0, torch.bfloat16
+    lens = [int(x) for x in rng.integers(0, 600, size=11)]
+    lens[3] = 0
+    if case == "prefix":
+        prefix = 96
+    elif case == "bs64":
+        bs, prefix = 64, 64
+    elif case == "f16":
+        dt = torch.float16
+    elif case == "crossings":
+        H, G, bs, prefix, lens = 14, 2, 32, 32, [333, 65, 1, 130]
+    c = make_prefill(len(lens), H, G, 128, bs, (1, 1), prefix=prefix, dtype=dt, seed=23,
+                     device=device, q_lens=lens)
+    if case == "v_huge":
+        c.v_new[5:9] *= 1e5  # beyond fp16 after widening: those items take the exact redo
+    write(c)
+    if case == "varlen":
+        c.kv_lens[4] = max(int(c.kv_lens[4]) - 3, 0)  # kv_len < q_len for one sequence
+
+    def go(mode):
+        out = torch.full((c.q.shape[0], H, 128), 7.0, dtype=torch.float32, device=device)
+        assert _lib.lib().flour_hip_set_prefill_dma(mode) == 0
+        try:
+            ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                               c.block_tables, c.max_seqlen_q, c.scale, block_size=bs,
+                               out_dtype=torch.float32, out=out)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_dma(1)
+        return out
+
+    a, b = go(2), go(0)
+    assert torch.equal(a, b)
+    ref, rows = oracle_prefill(c, seqs=[0, 1, 2])
+    rel = errors(to_np(a)[rows], ref)[1]
+    print(f"dma {case} rel_l2={rel:.3e}", flush=True)
+    assert rel <= 1e-3
+
+
+def test_prefill_dma_switch_rejects_bad_mode():
+    from flour_amd import _lib
+    assert _lib.lib().flour_hip_set_prefill_dma(3) != 0
+    assert _lib.lib().flour_hip_set_prefill_dma(-1) != 0
+
+
 @pytest.mark.parametrize("dt,H,G,D,bs,lens,prefix", [
     (torch.float32, 8, 8, 64, 16, [1, 17, 40, 300], 32),   # eight rows per workgroup
     (torch.float32, 16, 4, 128, 16, [129, 5], 0),           # two rows x four heads
