@@ -353,12 +353,14 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
-@pytest.mark.parametrize("case", ["varlen", "prefix", "bs64", "f16", "v_huge", "crossings"])
+@pytest.mark.parametrize("case", ["varlen", "prefix", "bs64", "f16", "v_huge", "crossings",
+                                  "short_items", "long"])
 def test_prefill_dma_staging_matches_register_staging(device, case):
     """Direct-to-LDS staging (K rows from the pool and V pages from a transposed fp16 staging
-    copy, both by buffer loads into LDS) gives bit-identical output to register staging:
-    ragged lengths with empty sequences and kv_len < q_len, prefix-cached kv, 64-token blocks,
-    fp16 pools, V outside the fp16 range (the exact-mode redo) and tiles straddling blocks."""
+    copy, both by buffer loads into LDS) gives bit-identical output to register staging: ragged lengths with empty sequences and
+    kv_len < q_len, prefix-cached kv, 64-token blocks, fp16 pools, V outside the fp16 range (the
+    exact-mode redo), tiles straddling blocks, items of one to three kv tiles, and a long
+    sequence whose block-table window moves."""
     from flour_amd import _lib
     rng = np.random.default_rng(17)
     H, G, bs, prefix, dt = 8, 2, 16, 0, torch.bfloat16
@@ -372,6 +374,10 @@ def test_prefill_dma_staging_matches_register_staging(device, case):
         dt = torch.float16
     elif case == "crossings":
         H, G, bs, prefix, lens = 14, 2, 32, 32, [333, 65, 1, 130]
+    elif case == "short_items":
+        lens = [1, 2, 63, 64, 65, 127, 128, 129, 191, 192]
+    elif case == "long":
+        H, G, lens = 4, 1, [4100, 70, 700]
     c = make_prefill(len(lens), H, G, 128, bs, (1, 1), prefix=prefix, dtype=dt, seed=23,
                      device=device, q_lens=lens)
     if case == "v_huge":
