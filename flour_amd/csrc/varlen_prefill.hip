@@ -178,6 +178,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     const int G = gridDim.x;
     const int wg = blockIdx.x;
     const int kv_cap = max_blocks * block_size;  // kv lengths are clamped to the block table
+    // DMA: pages per sequence in the V staging copy (the block table's capacity in whole tiles)
+    const int stage_pages = 4 * ((kv_cap + PF_KT - 1) / PF_KT);
 
     __shared__ int sched_order[PF_MAX_SEQS];       // sequences by decreasing tile count
     __shared__ int sched_more[PF_MAX_LEVELS + 1];  // [v]: sequences with more than v tiles
@@ -185,8 +187,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     __shared__ int sched_cum[PF_MAX_LEVELS + 2];   // [L]: items before level L
     __shared__ int sched_cu[PF_MAX_SEQS + 1];      // cu_seqlens
     __shared__ int sched_kv[PF_MAX_SEQS];          // clamped kv lengths
-    // DMA: first staging-copy page of each sequence (4 pages per 64-token kv tile)
-    __shared__ int sched_vpage[DMA ? PF_MAX_SEQS : 1];
     // query tiles of a sequence; one with kv_len < q_len still has its tiles, whose items
     // attend nothing and write zero rows (as the generic path and the oracle do)
     auto seq_tiles = [&](int sq) {
@@ -260,11 +260,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
                                     [&](int L, int x) { sched_cum[L] = x; }, false);
             if (lane == 0) sched_cum[NQ] = t;
-        }
-        if (DMA && w == 1) {
-            wave_scan(num_seqs,
-                      [&](int sq) { return 4 * ((max(sched_kv[sq], 0) + PF_KT - 1) / PF_KT); },
-                      [&](int sq, int x) { sched_vpage[sq] = x; }, false);
         }
         __syncthreads();
         total_base = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
@@ -365,7 +360,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             it.n_kt = uni(b.w);
             // (page 0 for an empty sequence: its loads are all masked, its table row exists)
             it.last_page = it.kv_len > 0 ? (BS16 ? (it.kv_len - 1) >> 4 : (it.kv_len - 1) / block_size) : 0;
-            if constexpr (DMA) it.vpage = uni(sched_vpage[it.seq]);
+            if constexpr (DMA) it.vpage = it.seq * stage_pages;
         }
         return it;
     };
@@ -999,52 +994,45 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 // Staging copy of V for the DMA kernel: every 16-token page of each sequence's kv range,
 // rounded up to whole 64-token tiles, as V^T in fp16 (128 dims x 16 tokens, token sigma16(k) at
 // position k; bf16 values times 2^8 by the same conversion as the register-staged path), tokens
-// past kv_len zero. Page p of sequence s and kv head h is at ((vpage(s) + p) * kv_heads + h)
-// * 4 KB, vpage(s) = the sum over earlier sequences of 4 * ceil(kv_len / 64), kv lengths clamped
-// to the block table. One 512-thread workgroup per 8 pages of one kv head.
-static constexpr int PF_STAGE_PAGES = 8;
+// past kv_len zero. Page p of sequence s and kv head h is at ((s * P + p) * kv_heads + h) * 4 KB,
+// P = 4 * ceil(max_blocks * block_size / 64) pages per sequence (the block table's capacity in
+// whole tiles). One four-wave workgroup per 64-token tile, one wave per page; tiles past a
+// sequence's kv range exit at once. The kv length and the page's block id are loaded
+// independently, so a page costs two dependent memory round trips (ids, then rows) before its
+// store, and every load and store instruction moves whole 256 B rows or 1 KB runs.
 template <typename T>
-__global__ __launch_bounds__(512) void prefill_v_stage_kernel(
+__global__ __launch_bounds__(256) void prefill_v_stage_kernel(
     f16_t* __restrict__ ws, const T* __restrict__ v_pool, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ block_tables, int max_blocks, int kv_heads, int block_size,
-    int64_t num_slots, int chunks_per_seq) {
-    __shared__ __attribute__((aligned(16))) uint16_t tp[PF_STAGE_PAGES][PF_D * 16];
-    __shared__ int s_base;
-    const int seq = blockIdx.x / chunks_per_seq;
-    const int p0 = (blockIdx.x - seq * chunks_per_seq) * PF_STAGE_PAGES;
+    int64_t num_slots, int pages_per_seq) {
+    __shared__ __attribute__((aligned(16))) uint16_t tp[4][PF_D * 16];
+    const int tiles_per_seq = pages_per_seq >> 2;
+    const int seq = blockIdx.x / tiles_per_seq;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int p = 4 * (blockIdx.x - seq * tiles_per_seq) + wv;
     const int kvh = blockIdx.y;
-    const int tid = threadIdx.x;
     const int kv_cap = max_blocks * block_size;
-    auto pages_of = [&](int sq) {
-        return 4 * ((max(min(kv_lens[sq], kv_cap), 0) + PF_KT - 1) / PF_KT);
-    };
-    const int kvl = max(min(kv_lens[seq], kv_cap), 0);
-    const int n_pages = pages_of(seq);
-    if (p0 >= n_pages) return;
-    if (tid < 64) {  // this sequence's first page
-        int acc = 0;
-        for (int s2 = tid; s2 < seq; s2 += 64) acc += pages_of(s2);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-        if (tid == 0) s_base = acc;
-    }
-    // thread (i, m, c) = (tid / 64, (tid / 16) % 4, tid % 16): page p0 + i, tokens 4m .. 4m + 3,
-    // dims 8c .. 8c + 7 (a page lies in one block: block sizes are multiples of 16). Tokens
-    // 4m + j sit at positions sigma16(4m) + j, so each dim's four values are one 8-byte store.
-    const int i = tid >> 6, m = (tid >> 4) & 3, c = tid & 15;
-    const int p = p0 + i;
+    const int lb = min((16 * p) / block_size, max_blocks - 1);  // the page lies in one block
+    const int kvl_raw = kv_lens[seq];
+    const int bid = block_tables[(int64_t)seq * max_blocks + lb];
+    const int kvl = max(min(kvl_raw, kv_cap), 0);
+    if (p >= 4 * ((kvl + PF_KT - 1) / PF_KT)) return;  // the whole workgroup (same tile)
+    // lane (m, c) = (lane / 16, lane % 16): tokens 4m .. 4m + 3, dims 8c .. 8c + 7. Tokens
+    // 4m + j sit at positions sigma16(4m) + j, so each dim's four values are one 8-byte LDS store.
+    const int m = lane >> 4, c = lane & 15;
     const int tok0 = 16 * p + 4 * m;
-    u32x4 v[4] = {};
-    if (p < n_pages && tok0 < kvl) {
-        const int lb = (16 * p) / block_size;
-        const int max_phys = (int)(num_slots / block_size - 1);
-        const int phys = min(max(block_tables[(int64_t)seq * max_blocks + lb], 0), max_phys);
-        const T* src = v_pool + ((int64_t)kvh * num_slots + (int64_t)phys * block_size +
-                                 (tok0 - lb * block_size)) * PF_D + 8 * c;
+    const int max_phys = (int)(num_slots / block_size - 1);
+    const int phys = min(max(bid, 0), max_phys);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(v_pool + (int64_t)kvh * num_slots * PF_D), (short)0,
+        (int)(num_slots * PF_D * (int64_t)sizeof(T)), BUF_DWORD3);
+    const uint32_t row0 = (uint32_t)(phys * block_size + (tok0 - lb * block_size));
+    u32x4 v[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (tok0 + j < kvl) v[j] = *reinterpret_cast<const u32x4*>(src + j * PF_D);
-    }
+    for (int j = 0; j < 4; j++)  // tokens past kv_len read zeros (out-of-range offset)
+        v[j] = __builtin_amdgcn_raw_buffer_load_b128(
+            rsrc, tok0 + j < kvl ? ((row0 + j) * PF_D + 8 * c) * (uint32_t)sizeof(T) : PF_OOR, 0,
+            BUF_NT);
     if constexpr (std::is_same<T, bf16_t>::value) {
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -1053,24 +1041,23 @@ __global__ __launch_bounds__(512) void prefill_v_stage_kernel(
                 v[j][x] = pack2<f16_t>(lo_f32<bf16_t>(v[j][x]) * PF_V_SCALE,
                                        hi_f32<bf16_t>(v[j][x]) * PF_V_SCALE);
     }
+    uint16_t* t = tp[wv];
     const int pos = sigma16(4 * m);
 #pragma unroll
     for (int x = 0; x < 4; x++) {
         // dims 8c + 2x (low halves) and 8c + 2x + 1 (high halves) of tokens 4m .. 4m + 3
-        *reinterpret_cast<u32x2*>(&tp[i][(8 * c + 2 * x) * 16 + pos]) =
+        *reinterpret_cast<u32x2*>(&t[(8 * c + 2 * x) * 16 + pos]) =
             u32x2{perm_lo16(v[0][x], v[1][x]), perm_lo16(v[2][x], v[3][x])};
-        *reinterpret_cast<u32x2*>(&tp[i][(8 * c + 2 * x + 1) * 16 + pos]) =
+        *reinterpret_cast<u32x2*>(&t[(8 * c + 2 * x + 1) * 16 + pos]) =
             u32x2{perm_hi16(v[0][x], v[1][x]), perm_hi16(v[2][x], v[3][x])};
     }
     __syncthreads();
-    // thread (i, d) = (tid / 64, tid % 64): dims 2d, 2d + 1 of page p0 + i, 64 contiguous bytes
-    const int d2 = 2 * (tid & 63);
-    if (p < n_pages) {
-        f16_t* dst = ws + ((int64_t)(s_base + p) * kv_heads + kvh) * (PF_D * 16) + d2 * 16;
-        const u32x4* src = reinterpret_cast<const u32x4*>(&tp[i][d2 * 16]);
+    // the page in four 1 KB runs
+    u32x4* dst = reinterpret_cast<u32x4*>(
+        ws + ((int64_t)(seq * pages_per_seq + p) * kv_heads + kvh) * (PF_D * 16));
+    const u32x4* src = reinterpret_cast<const u32x4*>(t);
 #pragma unroll
-        for (int x = 0; x < 4; x++) reinterpret_cast<u32x4*>(dst)[x] = src[x];
-    }
+    for (int x = 0; x < 4; x++) dst[lane + 64 * x] = src[lane + 64 * x];
 }
 
 static int g_prefill_persistent = 1;  // a tuning / test switch
@@ -1162,11 +1149,11 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
         void* ws = nullptr;
         if (want && persistent && ws_bytes <= PF_STAGE_MAX_BYTES &&
             stage_alloc(&ws, (size_t)ws_bytes, stream)) {
-            const int64_t chunks = (pages_per_seq + PF_STAGE_PAGES - 1) / PF_STAGE_PAGES;
-            prefill_v_stage_kernel<T><<<dim3((unsigned)(num_seqs * chunks), (unsigned)kv_heads),
-                                        dim3(512), 0, stream>>>(
+            prefill_v_stage_kernel<T><<<dim3((unsigned)(num_seqs * pages_per_seq / 4),
+                                             (unsigned)kv_heads),
+                                        dim3(256), 0, stream>>>(
                 static_cast<f16_t*>(ws), static_cast<const T*>(v_pool), kv_lens, bt, max_blocks,
-                kv_heads, block_size, num_slots, (int)chunks);
+                kv_heads, block_size, num_slots, (int)pages_per_seq);
             int rc = check_hip(hipGetLastError(), "varlen_prefill V staging launch");
             if (rc == FLOUR_OK) {
                 auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, true>
