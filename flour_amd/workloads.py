@@ -42,6 +42,10 @@ WORKLOADS: dict[str, dict] = {
     "prefill_bf16_prefix_qwen2_7b": dict(kind="prefill", num_seqs=16, num_heads=28, kv_heads=4,
                                          head_dim=128, block_size=16, q_len=(128, 512),
                                          prefix=1024, dtype=torch.bfloat16, seed=4),
+    # long prompts (Llama-3-8B heads): the direct-to-LDS staging path of the prefill kernel
+    "prefill_bf16_long_llama3_8b": dict(kind="prefill", num_seqs=2, num_heads=32, kv_heads=8,
+                                        head_dim=128, block_size=16, q_len=(8192, 8192),
+                                        prefix=0, dtype=torch.bfloat16, seed=7),
     "decode_bf16_long_llama3_70b": dict(kind="decode", batch=8, num_heads=64, kv_heads=8,
                                         head_dim=128, block_size=16, ctx=(16384, 32768),
                                         dtype=torch.bfloat16, seed=5),

@@ -406,6 +406,35 @@ def test_prefill_dma_staging_matches_register_staging(device, case):
     assert rel <= 1e-3
 
 
+def test_prefill_long_workload_dma_staging(device):
+    """The long-prompt workload (2 x 8,192 rows, Llama-3-8B heads) takes direct-to-LDS staging
+    by default: bit-identical to register staging, and its last 128 rows of sequence 1 (a
+    suffix over 8,064 earlier positions) against the oracle."""
+    from flour_amd import _lib
+    c = make_workload("prefill_bf16_long_llama3_8b", device=device)
+    write(c)
+
+    def go(mode):
+        assert _lib.lib().flour_hip_set_prefill_dma(mode) == 0
+        try:
+            out = run(c, torch.float32)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_dma(1)
+        return out
+
+    a, b = go(1), go(0)
+    assert torch.equal(a, b)
+    cu = to_np(c.cu_seqlens_q)
+    rows = np.arange(int(cu[2]) - 128, int(cu[2]))
+    ref = O.paged_attention(to_np(c.q)[rows], to_np(c.k_pool), to_np(c.v_pool),
+                            to_np(c.block_tables)[1:2], np.array([0, 128], dtype=np.int32),
+                            to_np(c.kv_lens)[1:2], c.block_size, c.scale, bf16=True)
+    max_abs, rel = errors(to_np(a)[rows], ref)
+    print(f"long workload last rows max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
 def test_prefill_dma_switch_rejects_bad_mode():
     from flour_amd import _lib
     assert _lib.lib().flour_hip_set_prefill_dma(3) != 0
