@@ -353,6 +353,52 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
+def test_prefill_persistent_schedule_with_exact_redo(device):
+    """Several items per workgroup, where an item's first K / V tiles and Q rows are fetched
+    while the item before it runs, and some items take the exact-mode redo (V rows of +-1e5
+    overflow the fp16 widening): bit-identical to one workgroup per item, and within the
+    scaled bounds of the oracle on sequences with and without the large rows."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(17)
+    lens = [int(x) for x in rng.integers(90, 700, size=60)]
+    lens[4] = 0
+    lens[9] = 20
+    c = make_prefill(len(lens), 16, 4, 128, 16, (1, 1), prefix=64, dtype=torch.bfloat16,
+                     seed=31, device=device, q_lens=lens)
+    vn = c.v_new.float()
+    cu = c.cu_seqlens_q.cpu().tolist()
+    big = [s for s in range(len(lens)) if s % 3 == 1 and lens[s] > 0]
+    for s in big:
+        vn[cu[s] + lens[s] // 2, :, :] *= 1e5
+    c.v_new.copy_(vn.to(torch.bfloat16))
+    write(c)
+    c.kv_lens[9] = 19  # kv_len < q_len: the sequence attends nothing
+
+    def go(persistent):
+        out = torch.full((c.q.shape[0], 16, 128), 7.0, dtype=torch.float32, device=device)
+        _lib.lib().flour_hip_set_prefill_persistent(persistent)
+        try:
+            ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                               c.block_tables, c.max_seqlen_q, c.scale, out_dtype=torch.float32,
+                               out=out)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_persistent(1)
+        return out
+
+    a, b = go(1), go(0)
+    assert torch.equal(a, b)
+    assert bool((a[cu[9]:cu[10]] == 0.0).all())
+    for s in (0, 59):  # no large rows: the unit-scale bounds
+        ref, rows = oracle_prefill(c, seqs=[s])
+        max_abs, rel = errors(to_np(a)[rows], ref)
+        print(f"persistent redo seq {s}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+        assert max_abs <= 2e-3 and rel <= 1e-3
+    for s in (big[0], big[-1]):
+        ref, rows = oracle_prefill(c, seqs=[s])
+        _check_scaled(to_np(a)[rows], ref, f"persistent redo seq {s}")
+
+
 @pytest.mark.parametrize("case", ["varlen", "prefix", "bs64", "f16", "v_huge", "crossings",
                                   "short_items", "long"])
 def test_prefill_dma_staging_matches_register_staging(device, case):
