@@ -689,18 +689,26 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                                 u32x2{pack2<TO>(x[4 * i] * inv, x[4 * i + 1] * inv),
                                       pack2<TO>(x[4 * i + 2] * inv, x[4 * i + 3] * inv)};
                         }
+                    // the four row reads go out together (one LDS wait), then the stores
+                    u32x4 rowv[4];
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; s4++) {
+                        const uint16_t* src = &stg[(rr + 8 * s4) * PF_OPITCH + 8 * cc];
+                        const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+                        const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 4);
+                        rowv[s4] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+                    }
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; s4++) asm volatile("" ::"v"(rowv[s4]));
 #pragma unroll
                     for (int s4 = 0; s4 < 4; s4++) {
                         const int r = rr + 8 * s4;
-                        const uint16_t* src = &stg[r * PF_OPITCH + 8 * cc];
-                        const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
-                        const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 4);
                         if (wr0 + r < ql) {
                             TO* dst = ob + (int64_t)r * o_st + 64 * half;
                             if constexpr (DMA)
-                                *reinterpret_cast<u32x4*>(dst) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+                                *reinterpret_cast<u32x4*>(dst) = rowv[s4];
                             else
-                                gstore_b128(dst, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                                gstore_b128(dst, rowv[s4]);
                         }
                     }
                 }
@@ -956,11 +964,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         start_tiles(std::false_type{});
     };
     // first window of item k, or of the last sequence's row if there is none (a valid address)
-    auto item_window = [&](int k) __attribute__((always_inline)) {
-        const Item it = fetch(k);
+    auto window_of = [&](const Item& it) __attribute__((always_inline)) {
         return load_window(block_tables + (int64_t)(it.valid ? it.seq : 0) * max_blocks, 0,
                            it.last_page + 1);
     };
+    auto item_window = [&](int k) __attribute__((always_inline)) { return window_of(fetch(k)); };
     // Item-end check of the fp16 path (CHECK_V): true if this wave's output block is not finite
     // or its largest |output| is below PF_MIN_TRUSTED (both in the 2^8-scaled accumulator:
     // |o| / l is 2^8 times the output).
@@ -1108,7 +1116,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                     const Item nq = fetch(k + 1);
                     if (nq.valid) dma_q(nq);
-                    win_nx = item_window(k + 1);
+                    win_nx = window_of(nq);
                     pf_base = (nq.valid && n_kt >= 3) ? n_kt + (n_kt & 1) : (1 << 30);
                     nx_kvh = nq.kvh;
                     nx_kv_len = nq.kv_len;
