@@ -1443,10 +1443,12 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
                          ((uintptr_t)v_pool % 16 == 0) && ((q_stride_tok * es) % 16 == 0) &&
                          ((q_stride_head * es) % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
                          ((o_stride_tok * oes) % 16 == 0) && ((o_stride_head * oes) % 16 == 0);
+    // (the Q rows of a wave are loaded with 32-bit offsets from its first row: 31 row strides)
     const bool mfma = (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
                       head_dim == PF_D && block_size % 16 == 0 && aligned &&
                       num_slots % block_size == 0 && scale > 0.0f &&
-                      num_slots * head_dim * 2 <= (int64_t)0x7fffffff;
+                      num_slots * head_dim * 2 <= (int64_t)0x7fffffff && q_stride_tok >= 0 &&
+                      q_stride_tok * es * 32 <= (int64_t)0x7fffffff;
     if (!mfma) {
         if (simt_supported(dtype, head_dim, q, q_stride_tok, q_stride_head, k_pool, v_pool))
             return launch_attn_simt(dtype, out_dtype, out, o_stride_tok, o_stride_head, q,
