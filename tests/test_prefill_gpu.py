@@ -353,6 +353,39 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
+@pytest.mark.parametrize("bs", [32, 48])
+def test_prefill_persistent_schedule_other_page_sizes(device, bs):
+    """Several items per workgroup with 32- and 48-token pages (a 64-token tile spans two or
+    three pages, and the next item's first tiles are located through its block-table window
+    while the current item runs): bit-identical to one workgroup per item, and against the
+    oracle on two sequences."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(5 + bs)
+    lens = [int(x) for x in rng.integers(1, 600, size=48)]
+    c = make_prefill(len(lens), 16, 4, 128, bs, (1, 1), prefix=2 * bs, dtype=torch.bfloat16,
+                     seed=40 + bs, device=device, q_lens=lens)
+    write(c)
+
+    def go(persistent):
+        out = torch.full((c.q.shape[0], 16, 128), 7.0, dtype=torch.float32, device=device)
+        _lib.lib().flour_hip_set_prefill_persistent(persistent)
+        try:
+            ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                               c.block_tables, c.max_seqlen_q, c.scale, block_size=bs,
+                               out_dtype=torch.float32, out=out)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_persistent(1)
+        return out
+
+    a, b = go(1), go(0)
+    assert torch.equal(a, b)
+    ref, rows = oracle_prefill(c, seqs=[0, 47])
+    max_abs, rel = errors(to_np(a)[rows], ref)
+    print(f"persistent bs={bs}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
 def test_prefill_persistent_schedule_with_exact_redo(device):
     """Several items per workgroup, where an item's first K / V tiles and Q rows are fetched
     while the item before it runs, and some items take the exact-mode redo (V rows of +-1e5
