@@ -11,8 +11,11 @@
 // Design (head_dim 128, block_size a multiple of 16):
 //  * One workgroup (8 waves) per (128-row query tile, pair of query heads that share a kv
 //    head, sequence); wave w owns 32 query rows of head w / 4, and every K/V tile staged in
-//    LDS serves both heads. Workgroups are issued in decreasing query-tile index (close to
-//    longest-first, spread over all XCDs).
+//    LDS serves both heads. By default one persistent workgroup per CU walks its share of the
+//    item list (decreasing query-tile index, close to longest-first, dealt as a snake); the
+//    next item's Q rows are staged in LDS during the current item and its first K/V tiles
+//    loaded by the current item's last steps. Without the persistent schedule, one workgroup
+//    per item, issued in the same order over all XCDs.
 //  * 64-token K/V tiles are gathered page by page through the block table into LDS with
 //    buffer loads (tokens past kv_len read zeros); the loads of tile t+2 are in flight while
 //    tile t is computed and tile t+1 is written to the other LDS buffer. K is stored row-major
