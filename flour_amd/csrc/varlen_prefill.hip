@@ -11,7 +11,8 @@
 // Design (head_dim 128, block_size a multiple of 16):
 //  * One workgroup (8 waves) per (128-row query tile, pair of query heads that share a kv
 //    head, sequence); wave w owns 32 query rows of head w / 4, and every K/V tile staged in
-//    LDS serves both heads. By default one persistent workgroup per CU walks its share of the
+//    LDS serves both heads. (Register staging: a sequence's last tile of at most 64 / 32 rows
+//    runs as 4 heads x 64 rows / 8 heads x 32 rows per workgroup instead.) By default one persistent workgroup per CU walks its share of the
 //    item list (decreasing query-tile index, close to longest-first, dealt as a snake); the
 //    next item's Q rows are staged in LDS during the current item and its first K/V tiles
 //    loaded by the current item's last steps. Without the persistent schedule, one workgroup
@@ -200,7 +201,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // staged kernel their LDS is then reused as the Q staging area: one 8 KB block per wave
     // (32 query rows x 256 B, the 16-byte chunk c of row r stored at chunk c ^ (r % 16)),
     // which receives the next item's rows during the current item and stages the output.
-    constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1;
+    // Register staging also shapes each sequence's last, partial query tile by its rows
+    // (FLEX): 4 heads x 64 rows or 8 heads x 32 rows per item instead of 2 heads x 128, which
+    // needs four more decode tables.
+    constexpr bool FLEX = !DMA;
+    constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1 +
+                               (FLEX ? 2 * (PF_MAX_SEQS + 1) + 2 * (PF_MAX_LEVELS + 2) : 0);
     constexpr int QSTAGE_BYTES = DMA ? 0 : PF_WAVES * 32 * PF_D * 2;
     constexpr int SCHED_BYTES = 4 * SCHED_INTS > QSTAGE_BYTES ? 4 * SCHED_INTS : QSTAGE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t sched_raw[SCHED_BYTES];
@@ -210,6 +216,13 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int* const sched_cum = sched_fill + (PF_MAX_LEVELS + 1);  // [L]: items before level L
     int* const sched_cu = sched_cum + (PF_MAX_LEVELS + 2);    // cu_seqlens
     int* const sched_kv = sched_cu + (PF_MAX_SEQS + 1);       // clamped kv lengths
+    // FLEX: [i] items of the last tiles of the sequences at order positions before i (p1: the
+    // multi-head part, p2: the one-head part); cum1 / cum2 [L]: items of the part before
+    // level L
+    int* const sched_p1 = sched_kv + PF_MAX_SEQS;
+    int* const sched_p2 = sched_p1 + (PF_MAX_SEQS + 1);
+    int* const sched_cum1 = sched_p2 + (PF_MAX_SEQS + 1);
+    int* const sched_cum2 = sched_cum1 + (PF_MAX_LEVELS + 2);
     // query tiles of a sequence; one with kv_len < q_len still has its tiles, whose items
     // attend nothing and write zero rows (as the generic path and the oracle do)
     auto seq_tiles = [&](int sq) {
@@ -241,7 +254,22 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         }
         return __shfl(incl, 63, 64);  // total
     };
-    int total_items = 0, total_base = 0;  // items; (level, sequence) pairs
+    // Heads per item of a tile with r rows (FLEX): 8 for at most 32 rows, 4 for at most 64, else
+    // 2, but at most the GQA group rounded up to a power of two, and always 2 for groups of 1
+    // or 2 heads. Its log2 (1 .. 3) is what the item table keeps.
+    auto shape_lg = [&](int r) {
+        if (!FLEX || n_rep <= 2 || r > 64) return 1;
+        const int cap = n_rep <= 4 ? 2 : 3;
+        return min(r <= 32 ? 3 : 2, cap);
+    };
+    // items of sequence s's last tile in part 1 (multi-head) or part 2 (one-head)
+    auto last_items = [&](int sq, bool part2) {
+        const int t = seq_tiles(sq);
+        const int lg = shape_lg(sched_cu[sq + 1] - sched_cu[sq] - PF_QT * (t - 1));
+        if (lg == 1) return kv_heads * (part2 ? (n_rep & 1) : (n_rep >> 1));
+        return part2 ? 0 : kv_heads * ((n_rep + (1 << lg) - 1) >> lg);
+    };
+    int total_items = 0, total_base = 0, total1 = 0;  // items; (level, sequence) pairs; part 1
     if (persistent) {
         for (int i = tid; i <= num_seqs; i += PF_THREADS) sched_cu[i] = cu_seqlens[i];
         for (int i = tid; i < num_seqs; i += PF_THREADS) sched_kv[i] = min(kv_lens[i], kv_cap);
@@ -277,20 +305,53 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
         }
         __syncthreads();
+        // FLEX: the sequences present are order positions 0 .. n_present - 1
+        const int n_present = __builtin_amdgcn_readfirstlane(sched_more[0]);
         if (w == 0) {
             // level L (tile qt = NQ-1-L) holds the sequences with more than qt tiles:
             // sched_cum[L] = sequences on the levels before L
             const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
                                     [&](int L, int x) { sched_cum[L] = x; }, false);
             if (lane == 0) sched_cum[NQ] = t;
+        } else if (FLEX && w == 1) {
+            const int t = wave_scan(n_present, [&](int i) { return last_items(sched_order[i], false); },
+                                    [&](int i, int x) { sched_p1[i] = x; }, false);
+            if (lane == 0) sched_p1[n_present] = t;
+        } else if (FLEX && w == 2) {
+            const int t = wave_scan(n_present, [&](int i) { return last_items(sched_order[i], true); },
+                                    [&](int i, int x) { sched_p2[i] = x; }, false);
+            if (lane == 0) sched_p2[n_present] = t;
         }
         __syncthreads();
         total_base = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
         total_items = npairs * total_base;
+        if constexpr (FLEX) {
+            // a level holds the sequences with more than qt tiles: first those whose tile at qt
+            // is full (more than qt + 1 tiles), then those whose last tile it is
+            const int f1 = kv_heads * (n_rep >> 1), f2 = kv_heads * (n_rep & 1);
+            auto level_items = [&](int L, const int* pp, int f) {
+                const int qt = NQ - 1 - L;
+                const int nf = sched_more[qt + 1], np_ = sched_more[qt];
+                return nf * f + pp[np_] - pp[nf];
+            };
+            if (w == 0) {
+                int t = wave_scan(NQ, [&](int L) { return level_items(L, sched_p1, f1); },
+                                  [&](int L, int x) { sched_cum1[L] = x; }, false);
+                if (lane == 0) sched_cum1[NQ] = t;
+            } else if (w == 1) {
+                int t = wave_scan(NQ, [&](int L) { return level_items(L, sched_p2, f2); },
+                                  [&](int L, int x) { sched_cum2[L] = x; }, false);
+                if (lane == 0) sched_cum2[NQ] = t;
+            }
+            __syncthreads();
+            total1 = __builtin_amdgcn_readfirstlane(sched_cum1[NQ]);
+            total_items = total1 + __builtin_amdgcn_readfirstlane(sched_cum2[NQ]);
+        }
     }
 
     // ---- this workgroup's items, decoded into LDS (one thread per item). An entry holds
-    // {seq, qt, kv head, pair in group, q0, q_len, kv_len, kv tiles}.
+    // {seq, qt, kv head, first head in group | log2(heads per item) << 16, q0, q_len, kv_len,
+    // kv tiles}.
     //  * persistent: the item list is longest-first in two parts: the two-head pairs of every
     //    level, then (odd n_rep) the one-head pairs, whose items cost about 0.7 of a two-head
     //    item. Within a part, items go level by level, sequences by decreasing tile count, then
@@ -312,8 +373,57 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             n_items = 1;
         }
         for (int k = tid; k < n_items; k += PF_THREADS) {
-            int seq, level, kvh, hj;
-            if (persistent) {
+            int seq, level, kvh, h0, lg = 1;  // h0: the item's first head in its GQA group
+            if (FLEX && persistent) {
+                // part 1: multi-head items, part 2: one-head items; within a part level by
+                // level, the full tiles of a level (constant items per sequence) before its
+                // last tiles (items by their shape)
+                const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
+                const bool part2 = idx >= total1;
+                const int ii = part2 ? idx - total1 : idx;
+                const int* cum = part2 ? sched_cum2 : sched_cum1;
+                const int* pp = part2 ? sched_p2 : sched_p1;
+                const int f = part2 ? np_lone : np_full;
+                int lo = 0, hi = NQ - 1;  // last level L with cum[L] <= ii
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (cum[mid] <= ii) lo = mid; else hi = mid - 1;
+                }
+                level = lo;
+                const int qt = NQ - 1 - lo;
+                const int off = ii - cum[lo];
+                const int nf = sched_more[qt + 1], nl = sched_more[qt];
+                int p;
+                // a full tile, or any tile of a level whose last tiles all have the full
+                // tiles' item count (f > 0 in both cases)
+                if (off < nf * f || (f > 0 && pp[nl] - pp[nf] == (nl - nf) * f)) {
+                    const int pos = off / f;
+                    seq = sched_order[pos];
+                    p = off - pos * f;
+                    if (pos >= nf) lg = shape_lg(sched_cu[seq + 1] - sched_cu[seq] - PF_QT * qt);
+                } else {  // a sequence's last tile: last order position with pp[pos] <= target
+                    const int target = pp[nf] + (off - nf * f);
+                    int l2 = nf, h2 = nl - 1;
+                    while (l2 < h2) {
+                        const int mid = (l2 + h2 + 1) >> 1;
+                        if (pp[mid] <= target) l2 = mid; else h2 = mid - 1;
+                    }
+                    seq = sched_order[l2];
+                    p = target - pp[l2];
+                    lg = shape_lg(sched_cu[seq + 1] - sched_cu[seq] - PF_QT * qt);
+                }
+                if (part2) {
+                    kvh = p;
+                    h0 = n_rep - 1;
+                } else if (lg == 1) {
+                    kvh = p / half_rep;
+                    h0 = 2 * (p - kvh * half_rep);
+                } else {
+                    const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
+                    kvh = p / g;
+                    h0 = (p - kvh * g) << lg;
+                }
+            } else if (persistent) {
                 const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
                 const int n_full = np_full * total_base;
                 const bool lone = idx >= n_full;
@@ -329,7 +439,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 seq = sched_order[key - sched_cum[lo]];
                 const int p = ii - np * key;
                 kvh = lone ? p : p / half_rep;
-                hj = lone ? half_rep : p - kvh * half_rep;
+                h0 = 2 * (lone ? half_rep : p - kvh * half_rep);
             } else {
                 const int per_rank = num_seqs * npairs;
                 level = wg / per_rank;
@@ -337,7 +447,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 seq = r / npairs;
                 const int hp = r - seq * npairs;
                 kvh = hp / pairs_per_kv;
-                hj = hp - kvh * pairs_per_kv;
+                h0 = 2 * (hp - kvh * pairs_per_kv);
             }
             const int q0 = persistent ? sched_cu[seq] : cu_seqlens[seq];
             const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - q0;
@@ -349,7 +459,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             e[0] = seq;
             e[1] = qt;
             e[2] = kvh;
-            e[3] = hj;
+            e[3] = h0 | (lg << 16);
             e[4] = q0;
             e[5] = ql;
             e[6] = kvl;
@@ -364,7 +474,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 
     // A work item (all fields workgroup-uniform); valid == 0 past the end of the list.
     struct Item {
-        int valid, seq, qt, kvh, hj, q0, ql, kv_len, n_kt, last_page, vpage;
+        int valid, seq, qt, kvh, h0, lg, q0, ql, kv_len, n_kt, last_page, vpage;
     };
     auto uni = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
     auto fetch = [&](int k) __attribute__((always_inline)) {
@@ -376,7 +486,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             it.seq = uni(a.x);
             it.qt = uni(a.y);
             it.kvh = uni(a.z);
-            it.hj = uni(a.w);
+            it.h0 = uni(a.w & 0xffff);
+            it.lg = uni(a.w >> 16);
             it.q0 = uni(b.x);
             it.ql = uni(b.y);
             it.kv_len = uni(b.z);
@@ -388,7 +499,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         return it;
     };
 
-    const int hsel = w >> 2;  // which head of the pair
+    // a wave's head in the item's group and its 32-row block: heads of 8 / hpi waves each
+    // (hpi = 1 << lg heads per item), so waves w and w + 4, which share a SIMD, take the same
+    // rows of two heads
+    auto wave_hl = [&](const Item& it) { return it.h0 + ((w << it.lg) >> 3); };
+    auto wave_rb = [&](const Item& it) { return w & ((8 >> it.lg) - 1); };
     const int max_phys = (int)(num_slots / block_size - 1);
     const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
 
@@ -585,12 +700,13 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int head = 0, q0 = 0, ql = 0, wr0 = 0, lim = 0, wave_lim = 0, wave_min_lim = 0;
     bool wave_active = false;
     auto set_compute = [&](const Item& it) {
-        head = it.kvh * n_rep + 2 * it.hj + hsel;
+        const int hl = wave_hl(it);
+        head = it.kvh * n_rep + hl;
         q0 = it.q0;
         ql = it.ql;
         const int off = it.kv_len - it.ql;
-        wr0 = it.qt * PF_QT + 32 * (w & 3);
-        wave_active = (2 * it.hj + hsel < n_rep) && wr0 < it.ql;
+        wr0 = it.qt * PF_QT + 32 * wave_rb(it);
+        wave_active = hl < n_rep && wr0 < it.ql;
         lim = off + min(wr0 + ql32, it.ql - 1);        // this lane's row sees kv j <= lim
         wave_lim = off + min(wr0 + 31, it.ql - 1);     // largest limit in the wave
         wave_min_lim = off + wr0;                      // smallest limit in the wave
@@ -599,9 +715,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // padded rows read a valid row)
     u32x4 qb[8];
     auto load_q = [&](const Item& it) __attribute__((always_inline)) {
-        const int hd = it.kvh * n_rep + 2 * it.hj + hsel;
-        const int hq = 2 * it.hj + hsel < n_rep ? hd : hd - 1;
-        const int row = min(it.qt * PF_QT + 32 * (w & 3) + ql32, it.ql - 1);
+        const int hq = it.kvh * n_rep + min(wave_hl(it), n_rep - 1);
+        const int row = min(it.qt * PF_QT + 32 * wave_rb(it) + ql32, it.ql - 1);
         const T* qp = q + (int64_t)(it.q0 + row) * q_st + (int64_t)hq * q_sh + 8 * h2;
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) qb[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
@@ -612,9 +727,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // to the sequence's last row like load_q.
     uint16_t* const qstage = reinterpret_cast<uint16_t*>(sched_raw) + w * (32 * PF_D);
     auto dma_q = [&](const Item& it) __attribute__((always_inline)) {
-        const int hd = it.kvh * n_rep + 2 * it.hj + hsel;
-        const int hq = 2 * it.hj + hsel < n_rep ? hd : hd - 1;
-        const int row0 = it.qt * PF_QT + 32 * (w & 3);
+        const int hq = it.kvh * n_rep + min(wave_hl(it), n_rep - 1);
+        const int row0 = it.qt * PF_QT + 32 * wave_rb(it);
         const int rb = min(row0, it.ql - 1);
         const T* qp = q + (int64_t)(it.q0 + rb) * q_st + (int64_t)hq * q_sh;
         const __amdgpu_buffer_rsrc_t q_rsrc =

@@ -353,6 +353,43 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
+@pytest.mark.parametrize("H,G", [(20, 4), (28, 4), (32, 4)])
+def test_prefill_partial_tile_shapes(device, H, G):
+    """A sequence's last query tile with at most 64 (32) rows runs as items of 4 (8) heads x
+    64 (32) rows instead of 2 heads x 128, with GQA groups of 5, 7 and 8 heads: bit-identical
+    to one workgroup per (tile, head pair), and against the oracle on short and long
+    sequences."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(H)
+    lens = []
+    for i in range(36):
+        full = int(rng.integers(0, 4)) * 128
+        tail = [int(rng.integers(1, 33)), int(rng.integers(33, 65)), int(rng.integers(65, 129))][i % 3]
+        lens.append(full + tail)
+    c = make_prefill(len(lens), H, G, 128, 16, (1, 1), prefix=64, dtype=torch.bfloat16,
+                     seed=50 + H, device=device, q_lens=lens)
+    write(c)
+
+    def go(persistent):
+        out = torch.full((c.q.shape[0], H, 128), 7.0, dtype=torch.float32, device=device)
+        _lib.lib().flour_hip_set_prefill_persistent(persistent)
+        try:
+            ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                               c.block_tables, c.max_seqlen_q, c.scale, out_dtype=torch.float32,
+                               out=out)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_persistent(1)
+        return out
+
+    a, b = go(1), go(0)
+    assert torch.equal(a, b)
+    ref, rows = oracle_prefill(c, seqs=[0, 1, 2, 35])
+    max_abs, rel = errors(to_np(a)[rows], ref)
+    print(f"partial tiles H={H} G={G}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
 def test_prefill_graph_replay_matches_eager(device):
     """Prefill captured in a HIP graph and replayed, with eager work and synchronisations
     between replays: each replay gives the eager result bit for bit (several items per
