@@ -12,7 +12,9 @@
 //  * One workgroup (8 waves) per (128-row query tile, pair of query heads that share a kv
 //    head, sequence); wave w owns 32 query rows of head w / 4, and every K/V tile staged in
 //    LDS serves both heads. (Register staging: a sequence's last tile of at most 64 / 32 rows
-//    runs as 4 heads x 64 rows / 8 heads x 32 rows per workgroup instead.) By default one persistent workgroup per CU walks its share of the
+//    runs as 4 heads x 64 rows / 8 heads x 32 rows per workgroup instead, and with an odd GQA
+//    group the last head of two consecutive tiles as 1 head x 256 rows.) By default one
+//    persistent workgroup per CU walks its share of the
 //    item list (decreasing query-tile index, close to longest-first, dealt as a snake); the
 //    next item's Q rows are staged in LDS during the current item and its first K/V tiles
 //    loaded by the current item's last steps. Without the persistent schedule, one workgroup
@@ -77,6 +79,8 @@ static constexpr float PF_LOG2E = 1.4426950408889634f;
 static constexpr int PF_MAX_SEQS = 2048;
 static constexpr int PF_MAX_LEVELS = 512;  // query tiles per sequence (65536 rows)
 static constexpr int PF_MAX_WG_ITEMS = 256;  // items per workgroup
+// (level, sequence) entries up to which register staging shapes its items per entry
+static constexpr int PF_FLEX_ENTRIES = 4096;
 
 __device__ __forceinline__ int swap_bits01(int x) {
     return (x & ~3) | ((x & 1) << 1) | ((x >> 1) & 1);
@@ -201,12 +205,13 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // staged kernel their LDS is then reused as the Q staging area: one 8 KB block per wave
     // (32 query rows x 256 B, the 16-byte chunk c of row r stored at chunk c ^ (r % 16)),
     // which receives the next item's rows during the current item and stages the output.
-    // Register staging also shapes each sequence's last, partial query tile by its rows
-    // (FLEX): 4 heads x 64 rows or 8 heads x 32 rows per item instead of 2 heads x 128, which
-    // needs four more decode tables.
+    // Register staging shapes items per (level, sequence) entry (FLEX): a sequence's last,
+    // partial query tile takes 4 heads x 64 rows or 8 heads x 32 rows per item instead of
+    // 2 heads x 128, and the one-head items of two consecutive tiles (odd GQA groups) share
+    // one item of 256 rows; two more decode tables.
     constexpr bool FLEX = !DMA;
     constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1 +
-                               (FLEX ? 2 * (PF_MAX_SEQS + 1) + 2 * (PF_MAX_LEVELS + 2) : 0);
+                               (FLEX ? 2 * (PF_FLEX_ENTRIES + 1) : 0);
     constexpr int QSTAGE_BYTES = DMA ? 0 : PF_WAVES * 32 * PF_D * 2;
     constexpr int SCHED_BYTES = 4 * SCHED_INTS > QSTAGE_BYTES ? 4 * SCHED_INTS : QSTAGE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t sched_raw[SCHED_BYTES];
@@ -216,13 +221,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int* const sched_cum = sched_fill + (PF_MAX_LEVELS + 1);  // [L]: items before level L
     int* const sched_cu = sched_cum + (PF_MAX_LEVELS + 2);    // cu_seqlens
     int* const sched_kv = sched_cu + (PF_MAX_SEQS + 1);       // clamped kv lengths
-    // FLEX: [i] items of the last tiles of the sequences at order positions before i (p1: the
-    // multi-head part, p2: the one-head part); cum1 / cum2 [L]: items of the part before
-    // level L
-    int* const sched_p1 = sched_kv + PF_MAX_SEQS;
-    int* const sched_p2 = sched_p1 + (PF_MAX_SEQS + 1);
-    int* const sched_cum1 = sched_p2 + (PF_MAX_SEQS + 1);
-    int* const sched_cum2 = sched_cum1 + (PF_MAX_LEVELS + 2);
+    // FLEX: [e] items before (level, sequence) entry e of the list, in part 1 (multi-head
+    // items) and part 2 (one-head items)
+    int* const sched_pc1 = sched_kv + PF_MAX_SEQS;
+    int* const sched_pc2 = sched_pc1 + (PF_FLEX_ENTRIES + 1);
+    static_assert(!FLEX || 4 * SCHED_INTS <= QSTAGE_BYTES, "decode tables fit the Q staging");
     // query tiles of a sequence; one with kv_len < q_len still has its tiles, whose items
     // attend nothing and write zero rows (as the generic path and the oracle do)
     auto seq_tiles = [&](int sq) {
@@ -262,14 +265,22 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         const int cap = n_rep <= 4 ? 2 : 3;
         return min(r <= 32 ? 3 : 2, cap);
     };
-    // items of sequence s's last tile in part 1 (multi-head) or part 2 (one-head)
-    auto last_items = [&](int sq, bool part2) {
+    // shape of tile qt of sequence sq (its last tile by its rows, the others 2 heads x 128)
+    auto tile_lg = [&](int sq, int qt, int t) {
+        return qt < t - 1 ? 1 : shape_lg(sched_cu[sq + 1] - sched_cu[sq] - PF_QT * qt);
+    };
+    // items of entry (sq, qt): part 1 multi-head items; part 2 (odd n_rep) one-head items of
+    // tiles of 2 heads x 128, tiles 2j and 2j + 1 sharing one (placed at the later one)
+    auto entry_items = [&](int sq, int qt, int& c1, int& c2) {
         const int t = seq_tiles(sq);
-        const int lg = shape_lg(sched_cu[sq + 1] - sched_cu[sq] - PF_QT * (t - 1));
-        if (lg == 1) return kv_heads * (part2 ? (n_rep & 1) : (n_rep >> 1));
-        return part2 ? 0 : kv_heads * ((n_rep + (1 << lg) - 1) >> lg);
+        const int lg = tile_lg(sq, qt, t);
+        c1 = kv_heads * (lg == 1 ? (n_rep >> 1) : ((n_rep + (1 << lg) - 1) >> lg));
+        const bool lone_here = (n_rep & 1) && lg == 1 &&
+                               ((qt & 1) || !(qt + 1 < t && tile_lg(sq, qt + 1, t) == 1));
+        c2 = lone_here ? kv_heads : 0;
     };
     int total_items = 0, total_base = 0, total1 = 0;  // items; (level, sequence) pairs; part 1
+    bool flex_on = false;
     if (persistent) {
         for (int i = tid; i <= num_seqs; i += PF_THREADS) sched_cu[i] = cu_seqlens[i];
         for (int i = tid; i < num_seqs; i += PF_THREADS) sched_kv[i] = min(kv_lens[i], kv_cap);
@@ -305,57 +316,94 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
         }
         __syncthreads();
-        // FLEX: the sequences present are order positions 0 .. n_present - 1
-        const int n_present = __builtin_amdgcn_readfirstlane(sched_more[0]);
         if (w == 0) {
             // level L (tile qt = NQ-1-L) holds the sequences with more than qt tiles:
             // sched_cum[L] = sequences on the levels before L
             const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
                                     [&](int L, int x) { sched_cum[L] = x; }, false);
             if (lane == 0) sched_cum[NQ] = t;
-        } else if (FLEX && w == 1) {
-            const int t = wave_scan(n_present, [&](int i) { return last_items(sched_order[i], false); },
-                                    [&](int i, int x) { sched_p1[i] = x; }, false);
-            if (lane == 0) sched_p1[n_present] = t;
-        } else if (FLEX && w == 2) {
-            const int t = wave_scan(n_present, [&](int i) { return last_items(sched_order[i], true); },
-                                    [&](int i, int x) { sched_p2[i] = x; }, false);
-            if (lane == 0) sched_p2[n_present] = t;
         }
         __syncthreads();
         total_base = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
         total_items = npairs * total_base;
-        if constexpr (FLEX) {
-            // a level holds the sequences with more than qt tiles: first those whose tile at qt
-            // is full (more than qt + 1 tiles), then those whose last tile it is
-            const int f1 = kv_heads * (n_rep >> 1), f2 = kv_heads * (n_rep & 1);
-            auto level_items = [&](int L, const int* pp, int f) {
-                const int qt = NQ - 1 - L;
-                const int nf = sched_more[qt + 1], np_ = sched_more[qt];
-                return nf * f + pp[np_] - pp[nf];
-            };
-            if (w == 0) {
-                int t = wave_scan(NQ, [&](int L) { return level_items(L, sched_p1, f1); },
-                                  [&](int L, int x) { sched_cum1[L] = x; }, false);
-                if (lane == 0) sched_cum1[NQ] = t;
-            } else if (w == 1) {
-                int t = wave_scan(NQ, [&](int L) { return level_items(L, sched_p2, f2); },
-                                  [&](int L, int x) { sched_cum2[L] = x; }, false);
-                if (lane == 0) sched_cum2[NQ] = t;
+        flex_on = FLEX && total_base <= PF_FLEX_ENTRIES;
+        if (flex_on) {
+            // exclusive prefix sums of the entries' item counts in list order (level by level,
+            // sequences in tile-count order): each thread walks a contiguous run of entries
+            const int per = (total_base + PF_THREADS - 1) / PF_THREADS;
+            const int e0 = min(tid * per, total_base), e1 = min(e0 + per, total_base);
+            int L = 0, hi = NQ - 1;  // level of entry e0: last L with sched_cum[L] <= e0
+            while (L < hi) {
+                const int mid = (L + hi + 1) >> 1;
+                if (sched_cum[mid] <= e0) L = mid; else hi = mid - 1;
+            }
+            const int L0 = L, i0 = e0 - sched_cum[L];
+            int s1 = 0, s2 = 0;
+            for (int e = e0, i = i0; e < e1; e++) {
+                int c1, c2;
+                entry_items(sched_order[i], NQ - 1 - L, c1, c2);
+                s1 += c1;
+                s2 += c2;
+                if (++i == sched_more[NQ - 1 - L]) {  // levels are never empty once started
+                    L++;
+                    i = 0;
+                }
+            }
+            int x1 = s1, x2 = s2;  // inclusive scan within the wave
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y1 = __shfl_up(x1, o, 64), y2 = __shfl_up(x2, o, 64);
+                if (lane >= o) {
+                    x1 += y1;
+                    x2 += y2;
+                }
+            }
+            if (lane == 63) {  // wave totals (sched_fill is free once the order is built)
+                sched_fill[2 * w] = x1;
+                sched_fill[2 * w + 1] = x2;
             }
             __syncthreads();
-            total1 = __builtin_amdgcn_readfirstlane(sched_cum1[NQ]);
-            total_items = total1 + __builtin_amdgcn_readfirstlane(sched_cum2[NQ]);
+            int b1 = 0, b2 = 0, t1 = 0, t2 = 0;
+            for (int v = 0; v < PF_WAVES; v++) {
+                const int a1 = sched_fill[2 * v], a2 = sched_fill[2 * v + 1];
+                if (v < w) {
+                    b1 += a1;
+                    b2 += a2;
+                }
+                t1 += a1;
+                t2 += a2;
+            }
+            int r1 = b1 + x1 - s1, r2 = b2 + x2 - s2;
+            L = L0;
+            for (int e = e0, i = i0; e < e1; e++) {
+                int c1, c2;
+                entry_items(sched_order[i], NQ - 1 - L, c1, c2);
+                sched_pc1[e] = r1;
+                sched_pc2[e] = r2;
+                r1 += c1;
+                r2 += c2;
+                if (++i == sched_more[NQ - 1 - L]) {
+                    L++;
+                    i = 0;
+                }
+            }
+            if (tid == 0) {
+                sched_pc1[total_base] = t1;
+                sched_pc2[total_base] = t2;
+            }
+            __syncthreads();
+            total1 = __builtin_amdgcn_readfirstlane(t1);
+            total_items = total1 + __builtin_amdgcn_readfirstlane(t2);
         }
     }
 
     // ---- this workgroup's items, decoded into LDS (one thread per item). An entry holds
     // {seq, qt, kv head, first head in group | log2(heads per item) << 16, q0, q_len, kv_len,
     // kv tiles}.
-    //  * persistent: the item list is longest-first in two parts: the two-head pairs of every
-    //    level, then (odd n_rep) the one-head pairs, whose items cost about 0.7 of a two-head
+    //  * persistent: the item list is longest-first in two parts: the multi-head items of every
+    //    level, then (odd n_rep) the one-head items, whose items cost about 0.7 of a two-head
     //    item. Within a part, items go level by level, sequences by decreasing tile count, then
-    //    pairs. The k-th item of workgroup b is number kG + b on even k and kG + G-1-b on odd k
+    //    heads; a one-head item of tiles qt - 1 and qt sits at tile qt's level. The k-th item of workgroup b is number kG + b on even k and kG + G-1-b on odd k
     //    (a snake over the list balances the workgroups without shared state);
     //  * otherwise: one workgroup per (level, sequence, pair); items past a sequence's last
     //    tile exit at once.
@@ -374,54 +422,44 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         }
         for (int k = tid; k < n_items; k += PF_THREADS) {
             int seq, level, kvh, h0, lg = 1;  // h0: the item's first head in its GQA group
-            if (FLEX && persistent) {
-                // part 1: multi-head items, part 2: one-head items; within a part level by
-                // level, the full tiles of a level (constant items per sequence) before its
-                // last tiles (items by their shape)
+            if (flex_on) {
+                // part 1: multi-head items, part 2: one-head items, each in list order; the
+                // entry of item idx is the last one whose prefix is <= its index in the part
                 const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
                 const bool part2 = idx >= total1;
                 const int ii = part2 ? idx - total1 : idx;
-                const int* cum = part2 ? sched_cum2 : sched_cum1;
-                const int* pp = part2 ? sched_p2 : sched_p1;
-                const int f = part2 ? np_lone : np_full;
-                int lo = 0, hi = NQ - 1;  // last level L with cum[L] <= ii
+                const int* pc = part2 ? sched_pc2 : sched_pc1;
+                int e = 0, he = total_base - 1;
+                while (e < he) {
+                    const int mid = (e + he + 1) >> 1;
+                    if (pc[mid] <= ii) e = mid; else he = mid - 1;
+                }
+                int lo = 0, hi = NQ - 1;  // last level L with sched_cum[L] <= e
                 while (lo < hi) {
                     const int mid = (lo + hi + 1) >> 1;
-                    if (cum[mid] <= ii) lo = mid; else hi = mid - 1;
+                    if (sched_cum[mid] <= e) lo = mid; else hi = mid - 1;
                 }
                 level = lo;
+                seq = sched_order[e - sched_cum[lo]];
                 const int qt = NQ - 1 - lo;
-                const int off = ii - cum[lo];
-                const int nf = sched_more[qt + 1], nl = sched_more[qt];
-                int p;
-                // a full tile, or any tile of a level whose last tiles all have the full
-                // tiles' item count (f > 0 in both cases)
-                if (off < nf * f || (f > 0 && pp[nl] - pp[nf] == (nl - nf) * f)) {
-                    const int pos = off / f;
-                    seq = sched_order[pos];
-                    p = off - pos * f;
-                    if (pos >= nf) lg = shape_lg(sched_cu[seq + 1] - sched_cu[seq] - PF_QT * qt);
-                } else {  // a sequence's last tile: last order position with pp[pos] <= target
-                    const int target = pp[nf] + (off - nf * f);
-                    int l2 = nf, h2 = nl - 1;
-                    while (l2 < h2) {
-                        const int mid = (l2 + h2 + 1) >> 1;
-                        if (pp[mid] <= target) l2 = mid; else h2 = mid - 1;
-                    }
-                    seq = sched_order[l2];
-                    p = target - pp[l2];
-                    lg = shape_lg(sched_cu[seq + 1] - sched_cu[seq] - PF_QT * qt);
-                }
+                const int p = ii - pc[e];
                 if (part2) {
                     kvh = p;
                     h0 = n_rep - 1;
-                } else if (lg == 1) {
-                    kvh = p / half_rep;
-                    h0 = 2 * (p - kvh * half_rep);
+                    if (qt & 1) {  // with tile qt - 1: 1 head x 256 rows from it
+                        lg = 0;
+                        level = lo + 1;
+                    }
                 } else {
-                    const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
-                    kvh = p / g;
-                    h0 = (p - kvh * g) << lg;
+                    lg = tile_lg(seq, qt, seq_tiles(seq));
+                    if (lg == 1) {
+                        kvh = p / half_rep;
+                        h0 = 2 * (p - kvh * half_rep);
+                    } else {
+                        const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
+                        kvh = p / g;
+                        h0 = (p - kvh * g) << lg;
+                    }
                 }
             } else if (persistent) {
                 const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
@@ -453,7 +491,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - q0;
             const int kvl = persistent ? sched_kv[seq] : min(kv_lens[seq], kv_cap);
             const int qt = NQ - 1 - level;
-            const int row_last = min(qt * PF_QT + PF_QT, ql) - 1;
+            const int row_last = min(qt * PF_QT + (256 >> lg), ql) - 1;  // the item's last row
             const bool ok = qt * PF_QT < ql;  // always true for persistent items
             int* e = sched_items[k];
             e[0] = seq;
