@@ -356,9 +356,10 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
 @pytest.mark.parametrize("H,G", [(20, 4), (28, 4), (32, 4)])
 def test_prefill_partial_tile_shapes(device, H, G):
     """A sequence's last query tile with at most 64 (32) rows runs as items of 4 (8) heads x
-    64 (32) rows instead of 2 heads x 128, with GQA groups of 5, 7 and 8 heads: bit-identical
-    to one workgroup per (tile, head pair), and against the oracle on short and long
-    sequences."""
+    64 (32) rows instead of 2 heads x 128, and with an odd group the last head of two
+    consecutive tiles as 1 head x 256 rows, with GQA groups of 5, 7 and 8 heads and sequences
+    of 1 to 4 tiles: bit-identical to one workgroup per (tile, head pair), and against the
+    oracle on short and long sequences."""
     from flour_amd import _lib
     rng = np.random.default_rng(H)
     lens = []
@@ -387,6 +388,37 @@ def test_prefill_partial_tile_shapes(device, H, G):
     ref, rows = oracle_prefill(c, seqs=[0, 1, 2, 35])
     max_abs, rel = errors(to_np(a)[rows], ref)
     print(f"partial tiles H={H} G={G}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+def test_prefill_long_entry_list_uses_plain_pairs(device):
+    """More (tile, sequence) entries than the per-entry item tables hold (1,100 sequences of 4
+    query tiles, 4,400 entries): the persistent list falls back to plain head pairs and stays
+    bit-identical to one workgroup per item, with an odd GQA group of 7."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(77)
+    lens = [int(x) for x in rng.integers(385, 513, size=1100)]
+    c = make_prefill(len(lens), 7, 1, 128, 16, (1, 1), prefix=16, dtype=torch.bfloat16,
+                     seed=78, device=device, q_lens=lens)
+    write(c)
+
+    def go(persistent):
+        out = torch.full((c.q.shape[0], 7, 128), 7.0, dtype=torch.float32, device=device)
+        _lib.lib().flour_hip_set_prefill_persistent(persistent)
+        try:
+            ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                               c.block_tables, c.max_seqlen_q, c.scale, out_dtype=torch.float32,
+                               out=out)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_persistent(1)
+        return out
+
+    a, b = go(1), go(0)
+    assert torch.equal(a, b)
+    ref, rows = oracle_prefill(c, seqs=[0, 549, 1099])
+    max_abs, rel = errors(to_np(a.float())[rows], ref)
+    print(f"long entry list: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
