@@ -325,11 +325,11 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     lens[5] = 0
     lens[11] = 1
     lens[20] = 690
-    lens[7] = 50
+    lens[7] = 300  # three tiles: with an odd group the first two share a one-head item
     c = make_prefill(len(lens), H, G, 128, 16, (1, 1), prefix=32, dtype=torch.bfloat16, seed=9,
                      device=device, q_lens=lens)
     write(c)
-    c.kv_lens[7] = 49  # kv_len < q_len: the sequence attends nothing
+    c.kv_lens[7] = 299  # kv_len < q_len: the sequence attends nothing
 
     def go(persistent):
         out = torch.full((c.q.shape[0], H, 128), 7.0, dtype=torch.float32, device=device)
