@@ -269,15 +269,17 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     auto tile_lg = [&](int sq, int qt, int t) {
         return qt < t - 1 ? 1 : shape_lg(sched_cu[sq + 1] - sched_cu[sq] - PF_QT * qt);
     };
-    // items of entry (sq, qt): part 1 multi-head items; part 2 (odd n_rep) one-head items of
-    // tiles of 2 heads x 128, tiles 2j and 2j + 1 sharing one (placed at the later one)
+    // items of entry (sq, qt). With an odd n_rep the last head of tiles of 2 heads x 128 is a
+    // one-head item, tiles 2j and 2j + 1 sharing one of 256 rows that costs about as much as
+    // a two-head item of tile 2j + 1. Part 1: the multi-head items, then at odd qt the shared
+    // one-head items; part 2: one-head items of a single tile (2j without tile 2j + 1).
     auto entry_items = [&](int sq, int qt, int& c1, int& c2) {
         const int t = seq_tiles(sq);
         const int lg = tile_lg(sq, qt, t);
-        c1 = kv_heads * (lg == 1 ? (n_rep >> 1) : ((n_rep + (1 << lg) - 1) >> lg));
-        const bool lone_here = (n_rep & 1) && lg == 1 &&
-                               ((qt & 1) || !(qt + 1 < t && tile_lg(sq, qt + 1, t) == 1));
-        c2 = lone_here ? kv_heads : 0;
+        const bool lone = (n_rep & 1) && lg == 1;
+        c1 = kv_heads * (lg == 1 ? (n_rep >> 1) : ((n_rep + (1 << lg) - 1) >> lg)) +
+             (lone && (qt & 1) ? kv_heads : 0);
+        c2 = lone && !(qt & 1) && !(qt + 1 < t && tile_lg(sq, qt + 1, t) == 1) ? kv_heads : 0;
     };
     int total_items = 0, total_base = 0, total1 = 0;  // items; (level, sequence) pairs; part 1
     bool flex_on = false;
@@ -401,9 +403,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // {seq, qt, kv head, first head in group | log2(heads per item) << 16, q0, q_len, kv_len,
     // kv tiles}.
     //  * persistent: the item list is longest-first in two parts: the multi-head items of every
-    //    level, then (odd n_rep) the one-head items, whose items cost about 0.7 of a two-head
-    //    item. Within a part, items go level by level, sequences by decreasing tile count, then
-    //    heads; a one-head item of tiles qt - 1 and qt sits at tile qt's level. The k-th item of workgroup b is number kG + b on even k and kG + G-1-b on odd k
+    //    level, then (odd n_rep) the one-head items of a single tile, which cost about 0.7 of a
+    //    two-head item. Within a part, items go level by level, sequences by decreasing tile
+    //    count, then heads; a one-head item of tiles qt - 1 and qt sits in part 1 after tile
+    //    qt's multi-head items. The k-th item of workgroup b is number kG + b on even k and kG + G-1-b on odd k
     //    (a snake over the list balances the workgroups without shared state);
     //  * otherwise: one workgroup per (level, sequence, pair); items past a sequence's last
     //    tile exit at once.
@@ -446,13 +449,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 if (part2) {
                     kvh = p;
                     h0 = n_rep - 1;
-                    if (qt & 1) {  // with tile qt - 1: 1 head x 256 rows from it
-                        lg = 0;
-                        level = lo + 1;
-                    }
                 } else {
                     lg = tile_lg(seq, qt, seq_tiles(seq));
-                    if (lg == 1) {
+                    if (lg == 1 && p >= kv_heads * half_rep) {  // 1 head x 256 rows from qt - 1
+                        kvh = p - kv_heads * half_rep;
+                        h0 = n_rep - 1;
+                        lg = 0;
+                        level = lo + 1;
+                    } else if (lg == 1) {
                         kvh = p / half_rep;
                         h0 = 2 * (p - kvh * half_rep);
                     } else {
