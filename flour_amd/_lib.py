@@ -46,6 +46,12 @@ SIGNATURES: dict[str, tuple] = {
                                           _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                           _c_int, _c_int, _c_int, _c_int, _c_i64, _c_f, _c_int,
                                           _vp]),
+    "flour_hip_varlen_prefill_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int,
+                                                         _c_int, ctypes.POINTER(ctypes.c_size_t)]),
+    "flour_hip_varlen_prefill_ws": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _c_i64,
+                                             _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_f,
+                                             _c_int, _vp, _c_sz, _vp]),
     # include/flour_cache.h
     "flour_block_allocator_create": (_c_int, [_c_int, _vp]),
     "flour_block_allocator_destroy": (None, [_vp]),

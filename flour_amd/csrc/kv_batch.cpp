@@ -50,8 +50,10 @@ struct KvBatchImpl {
     int32_t* h_plan = nullptr;
     hipEvent_t plan_done = nullptr;
     bool plan_pending = false;
-    void* d_ws = nullptr;
+    void* d_ws = nullptr;  // decode split-context partials
     size_t ws_bytes = 0;
+    void* d_pf_ws = nullptr;  // prefill V staging copy (long prompts)
+    size_t pf_ws_bytes = 0;
 
     bool planned = false, plan_decode = false;
     int plan_n = 0, plan_total = 0, plan_max_q = 0, plan_max_ctx = 0;
@@ -99,6 +101,7 @@ struct KvBatchImpl {
         if (d_plan) (void)hipFree(d_plan);
         if (h_plan) (void)hipHostFree(h_plan);
         if (d_ws) (void)hipFree(d_ws);
+        if (d_pf_ws) (void)hipFree(d_pf_ws);
     }
 
     int alloc_device() {
@@ -123,6 +126,15 @@ struct KvBatchImpl {
                                                   max_seq_len, &ws_bytes) != FLOUR_OK)
             return FLOUR_ERR_INVALID_ARGUMENT;
         if (ws_bytes && check_hip(hipMalloc(&d_ws, ws_bytes), "kv_batch: decode workspace"))
+            return FLOUR_ERR_HIP;
+        // The prefill staging copy serves steps whose rows average at least 1,536 per sequence
+        // (the only ones that take it), so at most max_tokens / 1,536 sequences.
+        const int pf_seqs = std::max(1, std::min(max_seqs, max_tokens / 1536));
+        if (flour_hip_varlen_prefill_workspace_size(pf_seqs, max_blocks, block_size, kv_heads,
+                                                    head_dim, dtype, &pf_ws_bytes) != FLOUR_OK)
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        if (pf_ws_bytes &&
+            check_hip(hipMalloc(&d_pf_ws, pf_ws_bytes), "kv_batch: prefill workspace"))
             return FLOUR_ERR_HIP;
         device = true;
         return FLOUR_OK;
@@ -577,11 +589,13 @@ extern "C" int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void
                                       x.num_slots, x.plan_max_ctx, scale, x.dtype, x.d_ws,
                                       x.ws_bytes, stream);
     }
-    return flour_hip_varlen_prefill(out, out_dtype, o_stride_tok, o_stride_head, q, q_stride_tok,
-                                    q_stride_head, x.k_pools[layer], x.v_pools[layer], x.d_cu(),
-                                    x.d_lens(), x.d_tables(), x.max_blocks, x.plan_n,
-                                    x.plan_max_q, x.plan_total, num_heads, x.kv_heads, x.head_dim,
-                                    x.block_size, x.num_slots, scale, x.dtype, stream);
+    return flour_hip_varlen_prefill_ws(out, out_dtype, o_stride_tok, o_stride_head, q,
+                                       q_stride_tok, q_stride_head, x.k_pools[layer],
+                                       x.v_pools[layer], x.d_cu(), x.d_lens(), x.d_tables(),
+                                       x.max_blocks, x.plan_n, x.plan_max_q, x.plan_total,
+                                       num_heads, x.kv_heads, x.head_dim, x.block_size,
+                                       x.num_slots, scale, x.dtype, x.d_pf_ws, x.pf_ws_bytes,
+                                       stream);
 }
 extern "C" int flour_kv_batch_pool(const flour_kv_batch* b, int layer, void** k_pool,
                                    void** v_pool, int64_t* num_slots) {

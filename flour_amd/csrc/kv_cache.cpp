@@ -49,8 +49,10 @@ struct KvCacheImpl {
     int32_t* h_meta = nullptr;  // pinned staging of the same layout
     hipEvent_t meta_done = nullptr;
     bool meta_pending = false;
-    void* d_ws = nullptr;
+    void* d_ws = nullptr;  // decode split-context partials
     size_t ws_bytes = 0;
+    void* d_pf_ws = nullptr;  // prefill V staging copy (long prompts)
+    size_t pf_ws_bytes = 0;
     void** d_pool_ptrs = nullptr;  // device copy of the K pool addresses, then the V ones
     void* d_stage = nullptr;       // bundle staging, whole logical blocks (allocated on use)
     size_t stage_bytes = 0;
@@ -88,6 +90,7 @@ struct KvCacheImpl {
         if (d_meta) (void)hipFree(d_meta);
         if (h_meta) (void)hipHostFree(h_meta);
         if (d_ws) (void)hipFree(d_ws);
+        if (d_pf_ws) (void)hipFree(d_pf_ws);
         if (d_pool_ptrs) (void)hipFree(d_pool_ptrs);
         if (d_stage) (void)hipFree(d_stage);
     }
@@ -114,6 +117,12 @@ struct KvCacheImpl {
                                                   &ws_bytes) != FLOUR_OK)
             return FLOUR_ERR_INVALID_ARGUMENT;
         if (ws_bytes && check_hip(hipMalloc(&d_ws, ws_bytes), "kv_cache: decode workspace"))
+            return FLOUR_ERR_HIP;
+        if (flour_hip_varlen_prefill_workspace_size(1, num_blocks, block_size, kv_heads, head_dim,
+                                                    dtype, &pf_ws_bytes) != FLOUR_OK)
+            return FLOUR_ERR_INVALID_ARGUMENT;
+        if (pf_ws_bytes &&
+            check_hip(hipMalloc(&d_pf_ws, pf_ws_bytes), "kv_cache: prefill workspace"))
             return FLOUR_ERR_HIP;
         std::vector<void*> ptrs(k_pools);
         ptrs.insert(ptrs.end(), v_pools.begin(), v_pools.end());
@@ -725,11 +734,12 @@ extern "C" int flour_kv_cache_attention(flour_kv_cache* c, int layer, const void
                                       x.kv_heads, x.head_dim, x.block_size, x.num_slots, len,
                                       scale, x.dtype, x.d_ws, x.ws_bytes, stream);
     }
-    return flour_hip_varlen_prefill(out, out_dtype, o_stride_tok, o_stride_head, q, q_stride_tok,
-                                    q_stride_head, x.k_pools[layer], x.v_pools[layer], x.d_cu(),
-                                    x.d_kv_len(), x.d_table(), max_blocks, 1, seq_q, seq_q,
-                                    num_heads, x.kv_heads, x.head_dim, x.block_size, x.num_slots,
-                                    scale, x.dtype, stream);
+    return flour_hip_varlen_prefill_ws(out, out_dtype, o_stride_tok, o_stride_head, q,
+                                       q_stride_tok, q_stride_head, x.k_pools[layer],
+                                       x.v_pools[layer], x.d_cu(), x.d_kv_len(), x.d_table(),
+                                       max_blocks, 1, seq_q, seq_q, num_heads, x.kv_heads,
+                                       x.head_dim, x.block_size, x.num_slots, scale, x.dtype,
+                                       x.d_pf_ws, x.pf_ws_bytes, stream);
 }
 
 extern "C" int flour_kv_cache_reset_sequence(flour_kv_cache* c) {

@@ -40,7 +40,6 @@
 #include <math.h>
 
 #include <algorithm>
-#include <mutex>
 #include <type_traits>
 
 #include "flour_common.h"
@@ -121,13 +120,17 @@ static constexpr int PF_VPAGE_BYTES = 16 * PF_D * 2;
 // rsrc.base + soff + voff and land at LDS byte lds + 16 L; lanes past the buffer's size write
 // zeros. Issued from inline asm so that the compiler's wait-count tracking, which knows nothing
 // of these loads, adds no waits for them to the LDS reads; every wait for them is explicit.
-// M0 is written here and nowhere else in the kernel.
+// M0 (the LDS destination) is written here; "m0" in the clobber list makes the compiler keep
+// no live value of its own in M0 across the statement. The s_nop 0 between the M0 write and the
+// load is the wait state a vector memory instruction that reads M0 needs after an SALU write of
+// M0 (the hardware does not interlock it, and the compiler's hazard tracking does not look
+// inside inline asm).
 __device__ __forceinline__ void dma_b128(uint32_t voff, __amdgpu_buffer_rsrc_t rsrc, uint32_t lds,
                                          uint32_t soff) {
     const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
     const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
-                 :: "v"(voff), "s"(rsrc), "s"(l), "s"(so) : "memory");
+                 :: "v"(voff), "s"(rsrc), "s"(l), "s"(so) : "memory", "m0");
 }
 // 16-byte global store issued from inline asm: the compiler's wait-count tracking does not see
 // it, so pending output stores never turn its waits for tile loads into full drains (loads and
@@ -1444,38 +1447,16 @@ static int device_cus() {
     return cached[dev];
 }
 
-// Stream-ordered allocation of the V staging copy from the device's default memory pool, whose
-// release threshold is raised once so that freed blocks stay cached for the next call. False
-// (and nothing allocated) when the stream is being captured into a graph, the device has no
-// memory pools or the allocation fails: the caller then takes the register-staged path.
-static bool stage_alloc(void** p, size_t bytes, hipStream_t stream) {
-    static std::once_flag once[64];
-    static int pools_ok[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
-        return false;
-    std::call_once(once[dev], [dev] {
-        int supported = 0;
-        hipMemPool_t pool = nullptr;
-        if (hipDeviceGetAttribute(&supported, hipDeviceAttributeMemoryPoolsSupported, dev) !=
-                hipSuccess ||
-            !supported || hipDeviceGetDefaultMemPool(&pool, dev) != hipSuccess) {
-            pools_ok[dev] = 0;
-            return;
-        }
-        uint64_t keep = UINT64_MAX;
-        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-        pools_ok[dev] = 1;
-    });
-    if (!pools_ok[dev]) return false;
-    if (hipMallocAsync(p, bytes, stream) != hipSuccess) {
-        (void)hipGetLastError();  // clear the failed call's error state
-        *p = nullptr;
-        return false;
-    }
-    return true;
+// Bytes of the V staging copy the direct-to-LDS path reads for a call with num_seqs sequences
+// and block-table rows of max_blocks pages of block_size tokens (kv_heads heads, head_dim 128):
+// every 16-token page of the block table's capacity in whole 64-token tiles, per sequence and
+// kv head. 0 when it exceeds PF_STAGE_MAX_BYTES (the staging copy's buffer resource holds a
+// 32-bit size).
+static int64_t prefill_stage_bytes(int64_t num_seqs, int64_t max_blocks, int64_t block_size,
+                                   int64_t kv_heads) {
+    const int64_t pages_per_seq = 4 * ((max_blocks * block_size + PF_KT - 1) / PF_KT);
+    const int64_t bytes = num_seqs * pages_per_seq * kv_heads * PF_VPAGE_BYTES;
+    return bytes <= PF_STAGE_MAX_BYTES ? bytes : 0;
 }
 
 template <typename T, typename TO, int PV>
@@ -1484,7 +1465,7 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
                                const int32_t* cu, const int32_t* kv_lens, const int32_t* bt,
                                int max_blocks, int num_seqs, int max_seqlen_q, int total_q,
                                int num_heads, int n_rep, int block_size, int64_t num_slots,
-                               float scale, hipStream_t stream) {
+                               float scale, void* ws, size_t ws_size, hipStream_t stream) {
     const int64_t n_qt = (max_seqlen_q + PF_QT - 1) / PF_QT;
     const int64_t items = n_qt * num_seqs * (num_heads / n_rep) * ((n_rep + 1) / 2);
     const int64_t cus = device_cus();
@@ -1497,35 +1478,30 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
     }
     if (grid == 0) return FLOUR_OK;
     if constexpr (PV == PV_F16) {
-        // DMA path: the V staging copy lives in a stream-ordered allocation (no host sync;
-        // calls on other streams get their own), then two launches.
+        // DMA path: the V staging copy lives in the caller's workspace; two launches, the
+        // staging pre-pass then the attention kernel.
         const int kv_heads = num_heads / n_rep;
         const int64_t pages_per_seq = 4 * (((int64_t)max_blocks * block_size + PF_KT - 1) / PF_KT);
-        const int64_t ws_bytes = (int64_t)num_seqs * pages_per_seq * kv_heads * PF_VPAGE_BYTES;
+        const int64_t need = prefill_stage_bytes(num_seqs, max_blocks, block_size, kv_heads);
         const bool want = g_prefill_dma == 2 ||
                           (g_prefill_dma == 1 && total_q >= (int64_t)PF_DMA_MIN_MEAN_Q * num_seqs);
-        void* ws = nullptr;
-        if (want && persistent && ws_bytes <= PF_STAGE_MAX_BYTES &&
-            stage_alloc(&ws, (size_t)ws_bytes, stream)) {
+        if (want && persistent && ws != nullptr && need > 0 && (int64_t)ws_size >= need) {
             prefill_v_stage_kernel<T><<<dim3((unsigned)(num_seqs * pages_per_seq / 4),
                                              (unsigned)kv_heads),
                                         dim3(256), 0, stream>>>(
                 static_cast<f16_t*>(ws), static_cast<const T*>(v_pool), kv_lens, bt, max_blocks,
                 kv_heads, block_size, num_slots, (int)pages_per_seq);
-            int rc = check_hip(hipGetLastError(), "varlen_prefill V staging launch");
-            if (rc == FLOUR_OK) {
-                auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, true>
-                                             : varlen_prefill_mfma_kernel<T, TO, PV, false, true>;
-                kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
-                    static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
-                    static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt,
-                    max_blocks, num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt,
-                    (int)persistent, scale * PF_LOG2E, static_cast<const f16_t*>(ws),
-                    (uint32_t)ws_bytes);
-                rc = check_hip(hipGetLastError(), "varlen_prefill launch");
-            }
-            const int frc = check_hip(hipFreeAsync(ws, stream), "varlen_prefill staging free");
-            return rc != FLOUR_OK ? rc : frc;
+            const int rc = check_hip(hipGetLastError(), "varlen_prefill V staging launch");
+            if (rc != FLOUR_OK) return rc;
+            auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, true>
+                                         : varlen_prefill_mfma_kernel<T, TO, PV, false, true>;
+            kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
+                static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
+                static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt,
+                max_blocks, num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt,
+                (int)persistent, scale * PF_LOG2E, static_cast<const f16_t*>(ws),
+                (uint32_t)need);
+            return check_hip(hipGetLastError(), "varlen_prefill launch");
         }
     }
     auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, false>
@@ -1566,15 +1542,14 @@ extern "C" int flour_hip_set_prefill_precise_p(int on) {
     return FLOUR_OK;
 }
 
-extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stride_tok,
-                                        int64_t o_stride_head, const void* q,
-                                        int64_t q_stride_tok, int64_t q_stride_head,
-                                        const void* k_pool, const void* v_pool,
-                                        const int32_t* cu_seqlens_q, const int32_t* kv_lens,
-                                        const int32_t* block_tables, int max_blocks_per_seq,
-                                        int num_seqs, int max_seqlen_q, int total_q,
-                                        int num_heads, int kv_heads, int head_dim, int block_size,
-                                        int64_t num_slots, float scale, int dtype, void* stream) {
+static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
+                               int64_t o_stride_head, const void* q, int64_t q_stride_tok,
+                               int64_t q_stride_head, const void* k_pool, const void* v_pool,
+                               const int32_t* cu_seqlens_q, const int32_t* kv_lens,
+                               const int32_t* block_tables, int max_blocks_per_seq, int num_seqs,
+                               int max_seqlen_q, int total_q, int num_heads, int kv_heads,
+                               int head_dim, int block_size, int64_t num_slots, float scale,
+                               int dtype, void* workspace, size_t workspace_bytes, void* stream) {
     clear_error();
     if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) {
         set_error("varlen_prefill: unknown dtype (%d, out %d)", dtype, out_dtype);
@@ -1626,11 +1601,13 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
                ? launch_prefill_mfma<T, TO, PV_HILO>(                                            \
                      out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
                      v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
-                     max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale, s)   \
+                     max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale,      \
+                     workspace, workspace_bytes, s)                                              \
                : launch_prefill_mfma<T, TO, PV_F16>(                                             \
                      out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
                      v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
-                     max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale, s)
+                     max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale,      \
+                     workspace, workspace_bytes, s)
     if (dtype == FLOUR_DTYPE_BF16) {
         if (out_dtype == FLOUR_DTYPE_F32) FLOUR_PF(bf16_t, float);
         if (out_dtype == FLOUR_DTYPE_BF16) FLOUR_PF(bf16_t, bf16_t);
@@ -1640,4 +1617,66 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
     if (out_dtype == FLOUR_DTYPE_BF16) FLOUR_PF(f16_t, bf16_t);
     FLOUR_PF(f16_t, f16_t);
 #undef FLOUR_PF
+}
+
+extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stride_tok,
+                                        int64_t o_stride_head, const void* q,
+                                        int64_t q_stride_tok, int64_t q_stride_head,
+                                        const void* k_pool, const void* v_pool,
+                                        const int32_t* cu_seqlens_q, const int32_t* kv_lens,
+                                        const int32_t* block_tables, int max_blocks_per_seq,
+                                        int num_seqs, int max_seqlen_q, int total_q,
+                                        int num_heads, int kv_heads, int head_dim, int block_size,
+                                        int64_t num_slots, float scale, int dtype, void* stream) {
+    return varlen_prefill_impl(out, out_dtype, o_stride_tok, o_stride_head, q, q_stride_tok,
+                               q_stride_head, k_pool, v_pool, cu_seqlens_q, kv_lens, block_tables,
+                               max_blocks_per_seq, num_seqs, max_seqlen_q, total_q, num_heads,
+                               kv_heads, head_dim, block_size, num_slots, scale, dtype, nullptr, 0,
+                               stream);
+}
+
+extern "C" int flour_hip_varlen_prefill_workspace_size(int num_seqs, int max_blocks_per_seq,
+                                                       int block_size, int kv_heads, int head_dim,
+                                                       int dtype, size_t* bytes) {
+    clear_error();
+    if (!bytes) {
+        set_error("varlen_prefill_workspace_size: null output");
+        return FLOUR_ERR_INVALID_ARGUMENT;
+    }
+    *bytes = 0;
+    if (num_seqs < 0 || max_blocks_per_seq <= 0 || block_size <= 0 || kv_heads <= 0 ||
+        head_dim <= 0 || !valid_dtype(dtype)) {
+        set_error("varlen_prefill_workspace_size: bad shape (seqs=%d max_blocks=%d bs=%d "
+                  "kv_heads=%d head_dim=%d dtype=%d)",
+                  num_seqs, max_blocks_per_seq, block_size, kv_heads, head_dim, dtype);
+        return FLOUR_ERR_INVALID_ARGUMENT;
+    }
+    // only 16-bit pools at head_dim 128 with 16-token-aligned pages take the staged path
+    if ((dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) && head_dim == PF_D &&
+        block_size % 16 == 0)
+        *bytes = (size_t)prefill_stage_bytes(num_seqs, max_blocks_per_seq, block_size, kv_heads);
+    return FLOUR_OK;
+}
+
+extern "C" int flour_hip_varlen_prefill_ws(void* out, int out_dtype, int64_t o_stride_tok,
+                                           int64_t o_stride_head, const void* q,
+                                           int64_t q_stride_tok, int64_t q_stride_head,
+                                           const void* k_pool, const void* v_pool,
+                                           const int32_t* cu_seqlens_q, const int32_t* kv_lens,
+                                           const int32_t* block_tables, int max_blocks_per_seq,
+                                           int num_seqs, int max_seqlen_q, int total_q,
+                                           int num_heads, int kv_heads, int head_dim,
+                                           int block_size, int64_t num_slots, float scale,
+                                           int dtype, void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+    if (workspace != nullptr && (uintptr_t)workspace % 256 != 0) {
+        clear_error();
+        set_error("varlen_prefill_ws: workspace must be 256-byte aligned");
+        return FLOUR_ERR_WORKSPACE;
+    }
+    return varlen_prefill_impl(out, out_dtype, o_stride_tok, o_stride_head, q, q_stride_tok,
+                               q_stride_head, k_pool, v_pool, cu_seqlens_q, kv_lens, block_tables,
+                               max_blocks_per_seq, num_seqs, max_seqlen_q, total_q, num_heads,
+                               kv_heads, head_dim, block_size, num_slots, scale, dtype, workspace,
+                               workspace_bytes, stream);
 }

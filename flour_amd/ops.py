@@ -138,8 +138,9 @@ def decode_workspace_bytes(batch: int, num_heads: int, kv_heads: int, head_dim: 
     return n.value
 
 
-class DecodeWorkspace:
-    """Device scratch for split-context decode partials; grows on demand and is reused.
+class Workspace:
+    """Device scratch for the kernels that take a workspace (split-context decode partials,
+    the prefill V staging copy); grows on demand and is reused.
 
     Calls sharing one workspace must not overlap in time (one stream, or explicit ordering).
     """
@@ -152,6 +153,9 @@ class DecodeWorkspace:
         if self.buf is None or self.buf.numel() < nbytes:
             self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self.buf
+
+
+DecodeWorkspace = Workspace
 
 
 _default_ws: dict[int, DecodeWorkspace] = {}
@@ -223,16 +227,32 @@ def prepare_paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Te
     return run
 
 
+def prefill_workspace_bytes(num_seqs: int, max_blocks_per_seq: int, block_size: int,
+                            kv_heads: int, head_dim: int, dtype: torch.dtype) -> int:
+    """Bytes of the V staging copy that varlen_prefill's long-prompt path reads (0 when no
+    call of this shape can take that path)."""
+    n = ctypes.c_size_t(0)
+    check(lib().flour_hip_varlen_prefill_workspace_size(num_seqs, max_blocks_per_seq, block_size,
+                                                        kv_heads, head_dim, dtype_code(dtype),
+                                                        ctypes.byref(n)))
+    return n.value
+
+
 def varlen_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                    cu_seqlens_q: torch.Tensor, kv_lens: torch.Tensor, block_tables: torch.Tensor,
                    max_seqlen_q: int, scale: float, block_size: int = 16,
                    out_dtype: torch.dtype | None = None,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None,
+                   workspace: Workspace | None = None) -> torch.Tensor:
     """Causal attention of packed query rows q (total_q, num_heads, head_dim) over the cache.
 
     Sequence s owns rows cu_seqlens_q[s]:cu_seqlens_q[s+1] and kv_lens[s] cached positions
     (its own new rows last). q may be any view with a unit last stride, e.g. the reference's
     head-major (num_heads, seq, head_dim) transposed to (seq, num_heads, head_dim).
+
+    Without ``workspace`` the call goes to flour_hip_varlen_prefill, which needs no device
+    memory beyond its arguments. With one, flour_hip_varlen_prefill_ws may stage V in it for
+    long prompts (the workspace grows to the size the call needs).
     """
     _need_cuda(q, k_pool, v_pool, cu_seqlens_q, kv_lens, block_tables)
     _need_i32(cu_seqlens_q, kv_lens, block_tables)
@@ -247,12 +267,17 @@ def varlen_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     if out is None:
         out = torch.empty((T, H, D), dtype=out_dtype, device=q.device)
     num_seqs = cu_seqlens_q.numel() - 1
-    check(lib().flour_hip_varlen_prefill(_ptr(out), dtype_code(out.dtype), out.stride(0),
-                                         out.stride(1), _ptr(q), q.stride(0), q.stride(1),
-                                         _ptr(k_pool), _ptr(v_pool), _ptr(cu_seqlens_q),
-                                         _ptr(kv_lens), _ptr(block_tables), block_tables.shape[1],
-                                         num_seqs, max_seqlen_q, T, H, G, D, block_size,
-                                         num_slots, float(scale), dtype_code(q.dtype), _stream()))
+    args = (_ptr(out), dtype_code(out.dtype), out.stride(0), out.stride(1), _ptr(q), q.stride(0),
+            q.stride(1), _ptr(k_pool), _ptr(v_pool), _ptr(cu_seqlens_q), _ptr(kv_lens),
+            _ptr(block_tables), block_tables.shape[1], num_seqs, max_seqlen_q, T, H, G, D,
+            block_size, num_slots, float(scale), dtype_code(q.dtype))
+    if workspace is None:
+        check(lib().flour_hip_varlen_prefill(*args, _stream()))
+    else:
+        nbytes = prefill_workspace_bytes(num_seqs, block_tables.shape[1], block_size, G, D,
+                                         q.dtype)
+        ws = workspace.get(nbytes)
+        check(lib().flour_hip_varlen_prefill_ws(*args, _ptr(ws), ws.numel(), _stream()))
     return out
 
 

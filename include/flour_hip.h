@@ -176,6 +176,8 @@ int flour_hip_paged_decode_noalloc(void* out, int out_dtype, const void* q, cons
  *   block_tables [num_seqs, max_blocks_per_seq] int32
  *   max_seqlen_q bounds the per-sequence query count; total_q = cu_seqlens_q[num_seqs].
  * The K/V of the new rows must already be in the pool (flour_hip_kv_write).
+ * This entry point allocates nothing and needs no workspace: the kernel gathers every K/V
+ * tile through registers into LDS.
  * ---------------------------------------------------------------------------------------- */
 int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stride_tok,
                              int64_t o_stride_head, const void* q, int64_t q_stride_tok,
@@ -185,6 +187,34 @@ int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stride_tok,
                              int max_seqlen_q, int total_q, int num_heads, int kv_heads,
                              int head_dim, int block_size, int64_t num_slots, float scale,
                              int dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Kernel (3) with a caller-owned workspace: flour_hip_varlen_prefill plus `workspace` (device
+ * memory, 256-byte aligned, no initialisation needed). Same arguments, results and
+ * replacement of paged_attention (cpu.rs:57-112, seq_q >= 1) as flour_hip_varlen_prefill.
+ *
+ * With long prompts (at least 1,536 new rows per sequence on average) over 16-bit pools at
+ * head_dim 128 the call stages V once into the workspace (every 16-token page of each
+ * sequence, widened to fp16 and transposed, by a pre-pass kernel on `stream`) and the
+ * attention kernel then loads both K and V tiles straight into LDS. Otherwise, or when
+ * workspace_bytes is below flour_hip_varlen_prefill_workspace_size() for the call's
+ * num_seqs and max_blocks_per_seq, the call runs exactly as flour_hip_varlen_prefill (the
+ * workspace is not touched). Nothing is allocated either way. Calls that share a workspace
+ * must not overlap in time.
+ * ---------------------------------------------------------------------------------------- */
+int flour_hip_varlen_prefill_workspace_size(int num_seqs, int max_blocks_per_seq,
+                                            int block_size, int kv_heads, int head_dim,
+                                            int dtype, size_t* bytes);
+
+int flour_hip_varlen_prefill_ws(void* out, int out_dtype, int64_t o_stride_tok,
+                                int64_t o_stride_head, const void* q, int64_t q_stride_tok,
+                                int64_t q_stride_head, const void* k_pool, const void* v_pool,
+                                const int32_t* cu_seqlens_q, const int32_t* kv_lens,
+                                const int32_t* block_tables, int max_blocks_per_seq,
+                                int num_seqs, int max_seqlen_q, int total_q, int num_heads,
+                                int kv_heads, int head_dim, int block_size, int64_t num_slots,
+                                float scale, int dtype, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,8 +1,8 @@
-"""The Rust binding that INTEGRATION.md gives a maintainer (the `flour-hip-sys` extern block and
-the `flour_kv_batch_*` block) declares every function exactly as include/flour_hip.h and
-include/flour_cache.h do: same names, same number of parameters, same kind of each parameter
-(pointer, 32-bit int, 64-bit int, size, float) and the same return kind. No Rust toolchain
-exists here, so this is what pins the binding to the ABI the library exports.
+"""The Rust FFI crate a maintainer would add to flour (`rust/flour-hip-sys`: Cargo.toml, build.rs,
+src/lib.rs) declares every function exactly as include/flour_hip.h and include/flour_cache.h
+do: same names, same number of parameters, same kind of each parameter (pointer, 32-bit int,
+64-bit int, size, float) and the same return kind. No Rust toolchain exists here, so this is
+what pins the binding to the ABI the library exports.
 """
 from __future__ import annotations
 
@@ -45,16 +45,17 @@ def _rust_kind(ty: str) -> str:
             "f32": "f32", "": "void"}[t]
 
 
+CRATE = ROOT / "rust" / "flour-hip-sys"
+
+
 def _rust_decls() -> dict[str, tuple[str, list[str]]]:
-    md = (ROOT / "INTEGRATION.md").read_text()
-    blocks = re.findall(r"```rust\n(.*?)```", md, flags=re.S)
+    src = (CRATE / "src" / "lib.rs").read_text()
     out = {}
-    for b in blocks:
-        for ext in re.findall(r'extern "C" \{(.*?)\n\}', b, flags=re.S):
-            for name, params, ret in re.findall(
-                    r"fn\s+(flour_\w+)\s*\((.*?)\)\s*(?:->\s*([^;]+))?;", ext, flags=re.S):
-                ps = [p.split(":", 1)[1] for p in params.split(",") if ":" in p]
-                out[name] = (_rust_kind(ret or ""), [_rust_kind(p) for p in ps])
+    for ext in re.findall(r'extern "C" \{(.*?)\n\}', src, flags=re.S):
+        for name, params, ret in re.findall(
+                r"fn\s+(flour_\w+)\s*\((.*?)\)\s*(?:->\s*([^;]+))?;", ext, flags=re.S):
+            ps = [p.split(":", 1)[1] for p in params.split(",") if ":" in p]
+            out[name] = (_rust_kind(ret or ""), [_rust_kind(p) for p in ps])
     return out
 
 
@@ -69,7 +70,16 @@ def test_rust_binding_matches_the_headers():
         assert ret == c_ret, f"{name}: returns {ret} vs {c_ret}"
 
 
-def test_rust_binding_covers_every_kernel_entry_point():
+def test_rust_binding_covers_every_declared_function():
     c, rust = _c_decls(), _rust_decls()
-    missing = sorted(n for n in c if n.startswith("flour_hip_") and n not in rust)
-    assert not missing, f"flour_hip.h functions without a Rust declaration: {missing}"
+    missing = sorted(n for n in c if n not in rust)
+    assert not missing, f"header functions without a Rust declaration: {missing}"
+
+
+def test_crate_builds_the_library_from_this_repository():
+    cargo = (CRATE / "Cargo.toml").read_text()
+    assert 'name = "flour-hip-sys"' in cargo and 'links = "flour_hip"' in cargo
+    build = (CRATE / "build.rs").read_text()
+    assert '"flour_amd.build"' in build and "rustc-link-lib=dylib=flour_hip" in build
+    # the package path build.rs resolves by default is this repository's root
+    assert (CRATE / "../.." / "flour_amd" / "build.py").resolve().is_file()

@@ -28,10 +28,10 @@ def write(c):
     ops.kv_write(c.k_new, c.v_new, c.k_pool, c.v_pool, c.slot_mapping)
 
 
-def run(c, out_dtype=None, q=None):
+def run(c, out_dtype=None, q=None, workspace=None):
     out = ops.varlen_prefill(c.q if q is None else q, c.k_pool, c.v_pool, c.cu_seqlens_q,
                              c.kv_lens, c.block_tables, c.max_seqlen_q, c.scale,
-                             block_size=c.block_size, out_dtype=out_dtype)
+                             block_size=c.block_size, out_dtype=out_dtype, workspace=workspace)
     torch.cuda.synchronize()
     return out
 
@@ -475,7 +475,7 @@ def test_prefill_persistent_schedule_other_page_sizes(device, bs):
         try:
             ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
                                c.block_tables, c.max_seqlen_q, c.scale, block_size=bs,
-                               out_dtype=torch.float32, out=out)
+                               out_dtype=torch.float32, out=out, workspace=ops.Workspace(device))
             torch.cuda.synchronize()
         finally:
             _lib.lib().flour_hip_set_prefill_persistent(1)
@@ -574,7 +574,7 @@ def test_prefill_dma_staging_matches_register_staging(device, case):
         try:
             ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
                                c.block_tables, c.max_seqlen_q, c.scale, block_size=bs,
-                               out_dtype=torch.float32, out=out)
+                               out_dtype=torch.float32, out=out, workspace=ops.Workspace(device))
             torch.cuda.synchronize()
         finally:
             _lib.lib().flour_hip_set_prefill_dma(1)
@@ -596,16 +596,22 @@ def test_prefill_long_workload_dma_staging(device):
     c = make_workload("prefill_bf16_long_llama3_8b", device=device)
     write(c)
 
+    ws = ops.Workspace(device)
+
     def go(mode):
         assert _lib.lib().flour_hip_set_prefill_dma(mode) == 0
         try:
-            out = run(c, torch.float32)
+            out = run(c, torch.float32, workspace=ws)
             torch.cuda.synchronize()
         finally:
             _lib.lib().flour_hip_set_prefill_dma(1)
         return out
 
-    a, b = go(1), go(0)
+    b = go(0)
+    ws.buf.fill_(0x7F)  # the staged path rewrites every page it reads
+    a = go(1)
+    assert ws.buf.numel() >= ops.prefill_workspace_bytes(2, c.block_tables.shape[1],
+                                                         c.block_size, 8, 128, c.q.dtype) > 0
     assert torch.equal(a, b)
     cu = to_np(c.cu_seqlens_q)
     rows = np.arange(int(cu[2]) - 128, int(cu[2]))
@@ -615,6 +621,80 @@ def test_prefill_long_workload_dma_staging(device):
     max_abs, rel = errors(to_np(a)[rows], ref)
     print(f"long workload last rows max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+def test_prefill_staged_path_under_graph_replay(device):
+    """The staged path (V pre-pass into the caller's workspace, then direct-to-LDS loads)
+    captured in a HIP graph and replayed, with eager work and a workspace overwrite between
+    replays: each replay equals the eager call bit for bit (no allocation or capture check on
+    the launch path, so nothing changes under capture)."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(31)
+    lens = [int(x) for x in rng.integers(300, 900, size=12)]
+    c = make_prefill(len(lens), 16, 4, 128, 16, (1, 1), prefix=32, dtype=torch.bfloat16,
+                     seed=33, device=device, q_lens=lens)
+    write(c)
+    ws = ops.Workspace(device)
+    out = torch.empty((c.q.shape[0], 16, 128), dtype=torch.bfloat16, device=device)
+
+    def step():
+        ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens, c.block_tables,
+                           c.max_seqlen_q, c.scale, block_size=c.block_size, out=out,
+                           workspace=ws)
+
+    assert _lib.lib().flour_hip_set_prefill_dma(2) == 0
+    try:
+        step()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        reg = run(c, torch.bfloat16)  # no workspace: register staging
+        assert torch.equal(eager, reg)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        for i in range(3):
+            out.zero_()
+            ws.buf.fill_(0x55)  # stale staging contents between replays
+            noise = torch.randn(1 << 20, device=device).sum()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {i} differs"
+            assert torch.isfinite(noise)
+    finally:
+        _lib.lib().flour_hip_set_prefill_dma(1)
+
+
+def test_prefill_workspace_too_small_uses_register_staging(device):
+    """A workspace below the size query's bytes is never touched: the call runs register
+    staging, bit-identical to the call without a workspace."""
+    from flour_amd import _lib
+    c = make_prefill(3, 8, 2, 128, 16, (1, 1), prefix=16, dtype=torch.bfloat16, seed=35,
+                     device=device, q_lens=[700, 300, 90])
+    write(c)
+    need = ops.prefill_workspace_bytes(3, c.block_tables.shape[1], 16, 2, 128, torch.bfloat16)
+    small = ops.Workspace(device)
+    small.buf = torch.full((need - 256,), 0x3C, dtype=torch.uint8, device=device)
+    assert _lib.lib().flour_hip_set_prefill_dma(2) == 0
+    try:
+        nb = c.block_tables.shape[1]
+        out = torch.empty((c.q.shape[0], 8, 128), dtype=torch.float32, device=device)
+        rc = _lib.lib().flour_hip_varlen_prefill_ws(
+            out.data_ptr(), 0, out.stride(0), out.stride(1), c.q.data_ptr(), c.q.stride(0),
+            c.q.stride(1), c.k_pool.data_ptr(), c.v_pool.data_ptr(), c.cu_seqlens_q.data_ptr(),
+            c.kv_lens.data_ptr(), c.block_tables.data_ptr(), nb, 3, c.max_seqlen_q,
+            c.q.shape[0], 8, 2, 128, 16, c.k_pool.shape[1], c.scale, 1, small.buf.data_ptr(),
+            small.buf.numel(), None)
+        assert rc == 0, _lib.last_error()
+        torch.cuda.synchronize()
+    finally:
+        _lib.lib().flour_hip_set_prefill_dma(1)
+    assert torch.equal(out, run(c, torch.float32))
+    assert bool((small.buf == 0x3C).all())
 
 
 def test_prefill_dma_switch_rejects_bad_mode():
