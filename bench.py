@@ -332,6 +332,71 @@ def bench_batch_decode(torch, steps: int, warmup: int, cpu: bool, cpu_seconds: f
     return r
 
 
+MIXED_STEP = dict(layers=4, decoding=60, prompts=4, num_heads=32, kv_heads=8, head_dim=128,
+                  block_size=16, ctx=(512, 4096), prompt=(128, 512), seed=7)
+
+
+def bench_mixed_step(torch, steps: int, warmup: int):
+    """One continuous-batching step in which 60 sequences decode one row each (contexts
+    U[512, 4096]) while 4 prompts of U[128, 512] rows prefill, listed interleaved, at the
+    Llama-3-8B attention shape (bf16, block 16): attention of the planned step timed with its
+    one-row sequences on the decode kernel (one decode launch + one prefill launch over the
+    packed rows) against every row on the prefill kernel. Four layers of pools rotate, so each
+    launch reads from HBM."""
+    from flour_amd import _lib
+    from flour_amd.kv_cache import KvBatch
+
+    c = MIXED_STEP
+    L, H, G, D, bs = (c[k] for k in ("layers", "num_heads", "kv_heads", "head_dim", "block_size"))
+    g = torch.Generator(device="cpu").manual_seed(c["seed"])
+    ctx = torch.randint(c["ctx"][0], c["ctx"][1] + 1, (c["decoding"],), generator=g).tolist()
+    pl = torch.randint(c["prompt"][0], c["prompt"][1] + 1, (c["prompts"],), generator=g).tolist()
+    nblk = sum(-(-n // bs) for n in ctx + pl) + len(ctx) + len(pl)
+    n_seq = len(ctx) + len(pl)
+    b = KvBatch(L, nblk, n_seq, -(-c["ctx"][1] // bs) * bs, sum(pl) + len(ctx), H, G, D,
+                torch.bfloat16, bs)
+    torch.manual_seed(c["seed"] + 1000)
+    for layer in range(L):
+        for p in b.pool(layer):
+            p.normal_()
+    dec = [b.add_sequence() for _ in ctx]
+    pro = [b.add_sequence() for _ in pl]
+    for s, n in zip(dec, ctx):
+        b.allocate_kv(s, n)
+    for s, n in zip(pro, pl):
+        b.allocate_kv(s, n)
+    # prompts at four places among the decoding sequences
+    order = dec[:5] + [pro[0]] + dec[5:20] + [pro[1]] + dec[20:33] + [pro[2]] + dec[33:] + [pro[3]]
+    qn = [pl[pro.index(s)] if s in pro else 1 for s in order]
+    b.plan(order, qn)
+    T = sum(qn)
+    dev = torch.device("cuda:0")
+    q = torch.randn((T, H, D), device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    scale = D ** -0.5
+    st = {"i": 0}
+
+    def attn():
+        b.attention(st["i"] % L, q, scale, out=out)
+        st["i"] += 1
+
+    split_ms = loop_timed(torch, attn, steps, warmup)
+    assert _lib.lib().flour_hip_set_batch_split(0) == 0
+    try:
+        whole_ms = loop_timed(torch, attn, steps, warmup)
+    finally:
+        _lib.lib().flour_hip_set_batch_split(1)
+    dec_bytes = sum(ctx) * G * D * 2 * 2 + len(ctx) * H * D * 2 * 2
+    pf_flops = sum(H * 4 * D * n * (n + 1) // 2 for n in pl)
+    del b
+    return {"decoding": len(ctx), "prompts": len(pl), "prompt_rows": pl,
+            "split_us": round(split_ms * 1e3, 2), "all_prefill_us": round(whole_ms * 1e3, 2),
+            "speedup": round(whole_ms / split_ms, 2), "decode_bytes": dec_bytes,
+            "prefill_flops": pf_flops,
+            "note": "attention of one planned step (one layer); split = one paged-decode launch "
+                    "over the 60 one-row sequences + one prefill launch over the 4 prompts"}
+
+
 def cpu_rope_baseline(case, theta: float):
     """Oracle RoPE + KV write over the whole batch on host copies; (median seconds, runs)."""
     import numpy as np
@@ -602,6 +667,17 @@ def main():
                           "data": "synthetic (seeded N(0,1) K/V)",
                           "config": dict(BUNDLE, workload=name), "bundle": r}), flush=True)
         return
+    if name == "mixed_step_llama3_8b":
+        r = bench_mixed_step(torch, args.steps, args.warmup)
+        print(json.dumps({"metric": "continuous-batching mixed step attention (60 decoding + 4 "
+                                    "prompts)", "value": r["split_us"], "unit": "us",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["split_us"] / 1e3, "higher_is_better": False,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                          "data": "synthetic (seeded N(0,1) pools and q)",
+                          "config": dict(MIXED_STEP, workload=name), "mixed_step": r}),
+              flush=True)
+        return
     if name == "decode_batch_llama3_8b":
         r = bench_batch_decode(torch, args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
         print(json.dumps({"metric": "continuous-batching decode steps (64 sequences x 32 layers)",
@@ -711,6 +787,8 @@ def main():
         extra["kv_bundle_llama3_8b"] = bench_bundle(torch, 5, 2, not args.no_cpu)
         torch.cuda.empty_cache()
         extra["decode_batch_llama3_8b"] = bench_batch_decode(torch, 10, 3, not args.no_cpu, 3.0)
+        torch.cuda.empty_cache()
+        extra["mixed_step_llama3_8b"] = bench_mixed_step(torch, 20, 5)
         torch.cuda.empty_cache()
         result["extra"] = extra
 

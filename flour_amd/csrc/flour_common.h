@@ -226,4 +226,31 @@ inline bool valid_dtype(int dtype) {
 // Check a HIP launch/runtime status; record an error and return FLOUR_ERR_HIP on failure.
 int check_hip(hipError_t e, const char* what);
 
+// Library-internal launchers with per-sequence row indices, for a mixed continuous-batching
+// step (kv_batch.cpp): its one-row sequences run as one paged-decode batch whose entry b reads
+// and writes packed row rows[b], and its longer sequences as one varlen prefill whose sequence
+// s starts at packed row q_rows[s]. Both need the matrix-core path and return
+// FLOUR_ERR_UNSUPPORTED before any launch otherwise.
+// Whether the matrix-core decode / prefill kernels take a shape (alignment of q / out / strides
+// aside for prefill, which the entry point checks with the pointers).
+bool decode_mfma_supported(int dtype, int head_dim, int block_size, int n_rep, int batch,
+                           int num_heads, int64_t num_slots, const void* q, const void* k_pool,
+                           const void* v_pool);
+bool prefill_mfma_supported(int dtype, int head_dim, int block_size, int64_t num_slots,
+                            float scale, int64_t q_stride_tok);
+int paged_decode_rows(void* out, int out_dtype, const void* q, const void* k_pool,
+                      const void* v_pool, const int32_t* block_tables, int max_blocks_per_seq,
+                      const int32_t* context_lens, const int32_t* rows, int batch, int num_heads,
+                      int kv_heads, int head_dim, int block_size, int64_t num_slots,
+                      int max_context_len, float scale, int dtype, void* workspace,
+                      size_t workspace_bytes, void* stream);
+int varlen_prefill_rows(void* out, int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,
+                        const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const void* k_pool, const void* v_pool, const int32_t* cu_seqlens_q,
+                        const int32_t* q_rows, const int32_t* kv_lens,
+                        const int32_t* block_tables, int max_blocks_per_seq, int num_seqs,
+                        int max_seqlen_q, int total_q, int num_heads, int kv_heads, int head_dim,
+                        int block_size, int64_t num_slots, float scale, int dtype,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 }  // namespace flour

@@ -12,9 +12,11 @@
 // A forward step is planned once, not per layer: plan() takes the step's sequences and the
 // number of new rows each brings, and uploads their block tables, kv lengths, cu_seqlens and the
 // slot mapping of the new rows through pinned staging. Every layer then calls write_kv (the KV
-// write kernel over the packed new rows) and attention (paged decode when every sequence brings
-// one row, varlen prefill otherwise) on those device arrays, as attention.rs:104-109 does for one
-// sequence.
+// write kernel over the packed new rows) and attention on those device arrays, as
+// attention.rs:104-109 does for one sequence: paged decode when every sequence brings one row,
+// varlen prefill when none does, and for a mixed step (sequences decoding while others bring a
+// prompt) one decode launch over the one-row sequences plus one prefill launch over the rest,
+// each reading and writing its rows of the packed layout through row indices.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
@@ -30,6 +32,10 @@
 
 namespace flour {
 namespace host {
+
+// 1: a mixed step's one-row sequences run on the decode kernel (default); 0: every row of a
+// mixed step on the prefill kernel. A tuning / test switch.
+static int g_batch_split = 1;
 
 struct KvBatchImpl {
     int num_layers, max_seqs, max_seq_len, max_tokens, num_heads, kv_heads, head_dim,
@@ -57,6 +63,10 @@ struct KvBatchImpl {
 
     bool planned = false, plan_decode = false;
     int plan_n = 0, plan_total = 0, plan_max_q = 0, plan_max_ctx = 0;
+    // mixed step: n_dec one-row sequences (longest context dec_max_ctx) and the longer ones
+    // (pf_max_q rows at most, pf_total in all)
+    bool plan_mixed = false;
+    int plan_n_dec = 0, plan_dec_max_ctx = 0, plan_pf_max_q = 0, plan_pf_total = 0;
 
     KvBatchImpl(int L, int nblk, int nseq, int max_len, int max_tok, int H, int G, int D, int bs,
                 int dt)
@@ -76,18 +86,31 @@ struct KvBatchImpl {
           tables(nseq, BlockTable(bs)),
           live(nseq, 0) {}
 
+    // A mixed step (one-row and longer sequences together) also uploads its tables and lengths
+    // again, one-row sequences first, with each entry's first packed row and the cu_seqlens of
+    // the longer sequences alone: [max_seqs x max_blocks] | [max_seqs] | [max_seqs] |
+    // [max_seqs + 1].
     int64_t plan_ints() const {
-        return (int64_t)max_seqs * max_blocks + max_seqs + max_seqs + 1 + 2 * (int64_t)max_tokens;
+        return (int64_t)max_seqs * max_blocks + max_seqs + max_seqs + 1 + 2 * (int64_t)max_tokens +
+               (int64_t)max_seqs * max_blocks + 3 * (int64_t)max_seqs + 1;
     }
     int32_t* d_tables() const { return d_plan; }
     int32_t* d_lens() const { return d_plan + (int64_t)max_seqs * max_blocks; }
     int32_t* d_cu() const { return d_lens() + max_seqs; }
     int32_t* d_slots() const { return d_cu() + max_seqs + 1; }
     int32_t* d_pos() const { return d_slots() + max_tokens; }
+    int32_t* d_mtab() const { return d_plan + off_mtab(); }
+    int32_t* d_mlens() const { return d_plan + off_mlens(); }
+    int32_t* d_mrows() const { return d_plan + off_mrows(); }
+    int32_t* d_mcu() const { return d_plan + off_mcu(); }
     int64_t off_lens() const { return (int64_t)max_seqs * max_blocks; }
     int64_t off_cu() const { return off_lens() + max_seqs; }
     int64_t off_slots() const { return off_cu() + max_seqs + 1; }
     int64_t off_pos() const { return off_slots() + max_tokens; }
+    int64_t off_mtab() const { return off_pos() + max_tokens; }
+    int64_t off_mlens() const { return off_mtab() + (int64_t)max_seqs * max_blocks; }
+    int64_t off_mrows() const { return off_mlens() + max_seqs; }
+    int64_t off_mcu() const { return off_mrows() + max_seqs; }
 
     ~KvBatchImpl() {
         if (plan_done) {
@@ -319,11 +342,41 @@ struct KvBatchImpl {
                 pos[k] = p;
             }
         }
+        // mixed step: the one-row sequences first (a decode batch), then the others (a prefill
+        // batch), each entry with its first packed row
+        int n_dec = 0, dec_max_ctx = 0, pf_max_q = 0;
+        for (int i = 0; i < n; i++) n_dec += q[i] == 1;
+        const bool mixed = n_dec > 0 && n_dec < n;
+        if (mixed) {
+            int32_t* mtab = h_plan + off_mtab();
+            int32_t* mlens = h_plan + off_mlens();
+            int32_t* mrows = h_plan + off_mrows();
+            int32_t* mcu = h_plan + off_mcu();
+            int jd = 0, jp = n_dec;
+            mcu[0] = 0;
+            for (int i = 0; i < n; i++) {
+                const int j = q[i] == 1 ? jd++ : jp++;
+                memcpy(mtab + (int64_t)j * max_blocks, tab + (int64_t)i * max_blocks,
+                       sizeof(int32_t) * (size_t)max_blocks);
+                mlens[j] = lens[i];
+                mrows[j] = cu[i];
+                if (q[i] == 1) {
+                    dec_max_ctx = std::max(dec_max_ctx, lens[i]);
+                } else {
+                    mcu[j - n_dec + 1] = mcu[j - n_dec] + q[i];
+                    pf_max_q = std::max(pf_max_q, q[i]);
+                }
+            }
+        }
         const struct {
             int64_t off, n;
-        } parts[5] = {{0, (int64_t)n * max_blocks}, {off_lens(), n}, {off_cu(), n + 1},
-                      {off_slots(), total}, {off_pos(), total}};
+        } parts[9] = {{0, (int64_t)n * max_blocks}, {off_lens(), n}, {off_cu(), n + 1},
+                      {off_slots(), total}, {off_pos(), total},
+                      {off_mtab(), mixed ? (int64_t)n * max_blocks : 0},
+                      {off_mlens(), mixed ? n : 0}, {off_mrows(), mixed ? n : 0},
+                      {off_mcu(), mixed ? n - n_dec + 1 : 0}};
         for (const auto& pr : parts)
+            if (pr.n > 0)
             if (check_hip(hipMemcpyAsync(d_plan + pr.off, h_plan + pr.off, pr.n * sizeof(int32_t),
                                          hipMemcpyHostToDevice, s),
                           "kv_batch: plan upload"))
@@ -336,6 +389,11 @@ struct KvBatchImpl {
         plan_total = (int)total;
         plan_max_q = max_q;
         plan_max_ctx = max_ctx;
+        plan_mixed = mixed;
+        plan_n_dec = n_dec;
+        plan_dec_max_ctx = dec_max_ctx;
+        plan_pf_max_q = pf_max_q;
+        plan_pf_total = (int)(total - n_dec);
         return FLOUR_OK;
     }
     // allocate_kv(ids[i], q[i]) for every sequence of the step, then plan(): all checks
@@ -589,6 +647,33 @@ extern "C" int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void
                                       x.num_slots, x.plan_max_ctx, scale, x.dtype, x.d_ws,
                                       x.ws_bytes, stream);
     }
+    // A mixed step runs its one-row sequences on the decode kernel and the rest on the prefill
+    // kernel (both over the packed rows, through row indices), when both take the shape.
+    const bool packed = q_stride_head == x.head_dim &&
+                        q_stride_tok == (int64_t)num_heads * x.head_dim &&
+                        o_stride_head == x.head_dim &&
+                        o_stride_tok == (int64_t)num_heads * x.head_dim;
+    const int n_pf = x.plan_n - x.plan_n_dec;
+    if (x.plan_mixed && g_batch_split && packed &&
+        decode_mfma_supported(x.dtype, x.head_dim, x.block_size, num_heads / x.kv_heads,
+                              x.plan_n_dec, num_heads, x.num_slots, q, x.k_pools[layer],
+                              x.v_pools[layer])) {
+        int rc = varlen_prefill_rows(
+            out, out_dtype, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head,
+            x.k_pools[layer], x.v_pools[layer], x.d_mcu(), x.d_mrows() + x.plan_n_dec,
+            x.d_mlens() + x.plan_n_dec, x.d_mtab() + (int64_t)x.plan_n_dec * x.max_blocks,
+            x.max_blocks, n_pf, x.plan_pf_max_q, x.plan_pf_total, num_heads, x.kv_heads,
+            x.head_dim, x.block_size, x.num_slots, scale, x.dtype, x.d_pf_ws, x.pf_ws_bytes,
+            stream);
+        if (rc == FLOUR_OK)
+            return paged_decode_rows(out, out_dtype, q, x.k_pools[layer], x.v_pools[layer],
+                                     x.d_mtab(), x.max_blocks, x.d_mlens(), x.d_mrows(),
+                                     x.plan_n_dec, num_heads, x.kv_heads, x.head_dim,
+                                     x.block_size, x.num_slots, x.plan_dec_max_ctx, scale,
+                                     x.dtype, x.d_ws, x.ws_bytes, stream);
+        if (rc != FLOUR_ERR_UNSUPPORTED) return rc;
+        clear_error();  // nothing launched: every row through the prefill kernel
+    }
     return flour_hip_varlen_prefill_ws(out, out_dtype, o_stride_tok, o_stride_head, q,
                                        q_stride_tok, q_stride_head, x.k_pools[layer],
                                        x.v_pools[layer], x.d_cu(), x.d_lens(), x.d_tables(),
@@ -607,5 +692,10 @@ extern "C" int flour_kv_batch_pool(const flour_kv_batch* b, int layer, void** k_
     *k_pool = b->b.k_pools[layer];
     *v_pool = b->b.v_pools[layer];
     *num_slots = b->b.num_slots;
+    return FLOUR_OK;
+}
+
+extern "C" int flour_hip_set_batch_split(int on) {
+    flour::host::g_batch_split = on ? 1 : 0;
     return FLOUR_OK;
 }

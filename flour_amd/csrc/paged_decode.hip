@@ -90,6 +90,10 @@ struct DecodeWs {
     float* ml;  // [2 * num_waves][n_rep][2] (max, sum) in the exp2 domain
     float* o;   // [2 * num_waves][n_rep][D]
     int* pre;   // [batch + 1] chunk prefix sums, written by workgroup 0 for the merge kernel
+    // row of q / out that batch entry b reads and writes: rows[b], or b when null (a mixed
+    // continuous-batching step runs its one-row sequences, scattered among the packed rows of
+    // longer ones, as one decode batch)
+    const int32_t* rows;
 };
 
 static int g_wg_override = 0;  // tuning / test hook: number of waves (0 = one resident round)
@@ -270,7 +274,8 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // Q^T as the B operand: lane (lg, lc) holds head lc, dims 32kk + 8lg .. +7.
     u32x4 qb[D / 32];
     auto load_q = [&](int b, int g) {
-        const T* qh = q + ((int64_t)b * num_heads + (int64_t)g * n_rep + lc) * D + 8 * lg;
+        const int64_t row = ws.rows ? (int64_t)ws.rows[b] : (int64_t)b;
+        const T* qh = q + (row * num_heads + (int64_t)g * n_rep + lc) * D + 8 * lg;
 #pragma unroll
         for (int kk = 0; kk < D / 32; kk++)
             qb[kk] = (lc < n_rep) ? *reinterpret_cast<const u32x4*>(qh + 32 * kk) : u32x4{0, 0, 0, 0};
@@ -376,7 +381,8 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
         lsum = sum_across_rows(lsum);
         if (lc < n_rep) {
             if (complete) {  // whole pair in this range: final output
-                TO* o = out + ((int64_t)b * num_heads + (int64_t)g * n_rep + lc) * D + (D / 4) * lg;
+                const int64_t row = ws.rows ? (int64_t)ws.rows[b] : (int64_t)b;
+                TO* o = out + (row * num_heads + (int64_t)g * n_rep + lc) * D + (D / 4) * lg;
                 const float inv = 1.0f / lsum;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
@@ -523,7 +529,8 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     // chunks before sequence b, of sequence b and in all sequences (the main kernel's sums)
     const int before = ws.pre[b], nch = ws.pre[b + 1] - before, all = ws.pre[batch];
-    TO* o = out + ((int64_t)b * num_heads + h) * D + E * lane;
+    const int64_t orow = ws.rows ? (int64_t)ws.rows[b] : (int64_t)b;
+    TO* o = out + (orow * num_heads + h) * D + E * lane;
     if (nch == 0) {
 #pragma unroll
         for (int i = 0; i < E; i++) o[i] = from_f32<TO>(0.0f);
@@ -698,7 +705,7 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
                              int num_heads, int kv_heads, int head_dim, int block_size,
                              int64_t num_slots, int max_context_len, float scale, int dtype,
                              void* workspace, size_t workspace_bytes, bool ws_from_scratch,
-                             void* stream);
+                             const int32_t* rows, void* stream);
 
 // ------------------------------------------------------------------ allocation-free variant
 // The split-context workspace of flour_hip_paged_decode_noalloc lives in this file-scope device
@@ -750,7 +757,7 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
     return flour::paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables,
                                     max_blocks_per_seq, context_lens, batch, num_heads, kv_heads,
                                     head_dim, block_size, num_slots, max_context_len, scale, dtype,
-                                    workspace, workspace_bytes, false, stream);
+                                    workspace, workspace_bytes, false, nullptr, stream);
 }
 
 extern "C" size_t flour_hip_paged_decode_noalloc_max_workspace(void) {
@@ -770,10 +777,20 @@ extern "C" int flour_hip_paged_decode_noalloc(void* out, int out_dtype, const vo
     return flour::paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables,
                                     max_blocks_per_seq, context_lens, batch, num_heads, kv_heads,
                                     head_dim, block_size, num_slots, max_context_len, scale, dtype,
-                                    nullptr, 0, true, stream);
+                                    nullptr, 0, true, nullptr, stream);
 }
 
 namespace flour {
+
+bool decode_mfma_supported(int dtype, int head_dim, int block_size, int n_rep, int batch,
+                           int num_heads, int64_t num_slots, const void* q, const void* k_pool,
+                           const void* v_pool) {
+    return (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
+           (head_dim == 128 || head_dim == 64) && block_size % 16 == 0 && n_rep <= 16 &&
+           batch <= DEC_MAX_BATCH && num_heads <= 65535 &&
+           num_slots * head_dim * 2 <= (int64_t)0x7fffffff && ((uintptr_t)q % 16 == 0) &&
+           ((uintptr_t)k_pool % 16 == 0) && ((uintptr_t)v_pool % 16 == 0);
+}
 
 static int paged_decode_impl(void* out, int out_dtype, const void* q, const void* k_pool,
                              const void* v_pool, const int32_t* block_tables,
@@ -781,7 +798,7 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
                              int num_heads, int kv_heads, int head_dim, int block_size,
                              int64_t num_slots, int max_context_len, float scale, int dtype,
                              void* workspace, size_t workspace_bytes, bool ws_from_scratch,
-                             void* stream) {
+                             const int32_t* rows, void* stream) {
     if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) {
         set_error("paged_decode: unknown dtype (%d, out %d)", dtype, out_dtype);
         return FLOUR_ERR_INVALID_ARGUMENT;
@@ -803,12 +820,12 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int n_rep = num_heads / kv_heads;
-    const bool mfma = (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
-                      (head_dim == 128 || head_dim == 64) && block_size % 16 == 0 && n_rep <= 16 &&
-                      batch <= DEC_MAX_BATCH && num_heads <= 65535 &&
-                      num_slots * head_dim * 2 <= (int64_t)0x7fffffff &&
-                      ((uintptr_t)q % 16 == 0) && ((uintptr_t)k_pool % 16 == 0) &&
-                      ((uintptr_t)v_pool % 16 == 0);
+    const bool mfma = decode_mfma_supported(dtype, head_dim, block_size, n_rep, batch, num_heads,
+                                            num_slots, q, k_pool, v_pool);
+    if (!mfma && rows) {
+        set_error("paged_decode: row indices need the matrix-core path");
+        return FLOUR_ERR_UNSUPPORTED;
+    }
     if (!mfma) {
         // one query row per sequence: cu_seqlens == nullptr
         const int64_t qs = (int64_t)num_heads * head_dim;
@@ -850,6 +867,7 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
     ws.pre = reinterpret_cast<int*>(
         reinterpret_cast<char*>(ws.o) +
         align256((size_t)2 * nwg * n_rep * (size_t)head_dim * sizeof(float)));
+    ws.rows = rows;
 #define FLOUR_DEC(T)                                                                            \
     do {                                                                                        \
         if (out_dtype == FLOUR_DTYPE_F32)                                                       \
@@ -871,6 +889,30 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
     if (dtype == FLOUR_DTYPE_BF16) FLOUR_DEC(bf16_t);
     FLOUR_DEC(f16_t);
 #undef FLOUR_DEC
+}
+
+}  // namespace flour
+
+namespace flour {
+
+// Paged decode whose batch entry b reads q row rows[b] and writes out row rows[b] of a packed
+// (rows, num_heads, head_dim) contiguous layout: the one-row sequences of a mixed
+// continuous-batching step. Matrix-core shapes only (FLOUR_ERR_UNSUPPORTED otherwise, before
+// any launch).
+int paged_decode_rows(void* out, int out_dtype, const void* q, const void* k_pool,
+                      const void* v_pool, const int32_t* block_tables, int max_blocks_per_seq,
+                      const int32_t* context_lens, const int32_t* rows, int batch, int num_heads,
+                      int kv_heads, int head_dim, int block_size, int64_t num_slots,
+                      int max_context_len, float scale, int dtype, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    if (!rows) {
+        set_error("paged_decode_rows: null row indices");
+        return FLOUR_ERR_INVALID_ARGUMENT;
+    }
+    return paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables, max_blocks_per_seq,
+                             context_lens, batch, num_heads, kv_heads, head_dim, block_size,
+                             num_slots, max_context_len, scale, dtype, workspace, workspace_bytes,
+                             false, rows, stream);
 }
 
 }  // namespace flour

@@ -156,7 +156,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ block_tables, int max_blocks, int num_seqs, int num_heads,
     int n_rep, int block_size, int64_t num_slots, int n_qt_max, int persistent,
-    float scale_log2, const f16_t* __restrict__ v_stage, uint32_t v_stage_bytes) {
+    float scale_log2, const f16_t* __restrict__ v_stage, uint32_t v_stage_bytes,
+    const int32_t* __restrict__ q_rows) {
     // DMA: K and V tiles go straight from memory into LDS (K from the pool, V from the staging
     // copy), three buffers, no staging registers. It needs the persistent schedule and fp16 P.V.
     static_assert(!DMA || PV == PV_F16, "the DMA kernel runs the fp16 P.V path");
@@ -494,7 +495,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 kvh = hp / pairs_per_kv;
                 h0 = 2 * (hp - kvh * pairs_per_kv);
             }
-            const int q0 = persistent ? sched_cu[seq] : cu_seqlens[seq];
+            // first q / out row of the sequence: q_rows[seq] when given (the sequences of a
+            // mixed step, whose rows sit among other sequences' rows), else its cu_seqlens start
+            const int q0 = q_rows ? q_rows[seq] : persistent ? sched_cu[seq] : cu_seqlens[seq];
             const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - q0;
             const int kvl = persistent ? sched_kv[seq] : min(kv_lens[seq], kv_cap);
             const int qt = NQ - 1 - level;
@@ -1465,7 +1468,8 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
                                const int32_t* cu, const int32_t* kv_lens, const int32_t* bt,
                                int max_blocks, int num_seqs, int max_seqlen_q, int total_q,
                                int num_heads, int n_rep, int block_size, int64_t num_slots,
-                               float scale, void* ws, size_t ws_size, hipStream_t stream) {
+                               float scale, void* ws, size_t ws_size, const int32_t* q_rows,
+                               hipStream_t stream) {
     const int64_t n_qt = (max_seqlen_q + PF_QT - 1) / PF_QT;
     const int64_t items = n_qt * num_seqs * (num_heads / n_rep) * ((n_rep + 1) / 2);
     const int64_t cus = device_cus();
@@ -1500,7 +1504,7 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
                 static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt,
                 max_blocks, num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt,
                 (int)persistent, scale * PF_LOG2E, static_cast<const f16_t*>(ws),
-                (uint32_t)need);
+                (uint32_t)need, q_rows);
             return check_hip(hipGetLastError(), "varlen_prefill launch");
         }
     }
@@ -1510,7 +1514,7 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
         static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
         static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt, max_blocks,
         num_seqs, num_heads, n_rep, block_size, num_slots, (int)n_qt, (int)persistent,
-        scale * PF_LOG2E, nullptr, 0u);
+        scale * PF_LOG2E, nullptr, 0u, q_rows);
     return check_hip(hipGetLastError(), "varlen_prefill launch");
 }
 
@@ -1542,6 +1546,19 @@ extern "C" int flour_hip_set_prefill_precise_p(int on) {
     return FLOUR_OK;
 }
 
+namespace flour {
+
+bool prefill_mfma_supported(int dtype, int head_dim, int block_size, int64_t num_slots,
+                            float scale, int64_t q_stride_tok) {
+    // (the Q rows of a wave are loaded with 32-bit offsets from its first row: 31 row strides)
+    return (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) && head_dim == PF_D &&
+           block_size % 16 == 0 && num_slots % block_size == 0 && scale > 0.0f &&
+           num_slots * head_dim * 2 <= (int64_t)0x7fffffff && q_stride_tok >= 0 &&
+           q_stride_tok * 2 * 32 <= (int64_t)0x7fffffff;
+}
+
+}  // namespace flour
+
 static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
                                int64_t o_stride_head, const void* q, int64_t q_stride_tok,
                                int64_t q_stride_head, const void* k_pool, const void* v_pool,
@@ -1549,7 +1566,8 @@ static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
                                const int32_t* block_tables, int max_blocks_per_seq, int num_seqs,
                                int max_seqlen_q, int total_q, int num_heads, int kv_heads,
                                int head_dim, int block_size, int64_t num_slots, float scale,
-                               int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+                               int dtype, void* workspace, size_t workspace_bytes,
+                               const int32_t* q_rows, void* stream) {
     clear_error();
     if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) {
         set_error("varlen_prefill: unknown dtype (%d, out %d)", dtype, out_dtype);
@@ -1578,11 +1596,12 @@ static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
                          ((q_stride_head * es) % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
                          ((o_stride_tok * oes) % 16 == 0) && ((o_stride_head * oes) % 16 == 0);
     // (the Q rows of a wave are loaded with 32-bit offsets from its first row: 31 row strides)
-    const bool mfma = (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
-                      head_dim == PF_D && block_size % 16 == 0 && aligned &&
-                      num_slots % block_size == 0 && scale > 0.0f &&
-                      num_slots * head_dim * 2 <= (int64_t)0x7fffffff && q_stride_tok >= 0 &&
-                      q_stride_tok * es * 32 <= (int64_t)0x7fffffff;
+    const bool mfma = aligned && prefill_mfma_supported(dtype, head_dim, block_size, num_slots,
+                                                        scale, q_stride_tok);
+    if (!mfma && q_rows) {
+        set_error("varlen_prefill: row indices need the matrix-core path");
+        return FLOUR_ERR_UNSUPPORTED;
+    }
     if (!mfma) {
         if (simt_supported(dtype, head_dim, q, q_stride_tok, q_stride_head, k_pool, v_pool))
             return launch_attn_simt(dtype, out_dtype, out, o_stride_tok, o_stride_head, q,
@@ -1602,12 +1621,12 @@ static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
                      out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
                      v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
                      max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale,      \
-                     workspace, workspace_bytes, s)                                              \
+                     workspace, workspace_bytes, q_rows, s)                                      \
                : launch_prefill_mfma<T, TO, PV_F16>(                                             \
                      out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
                      v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
                      max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale,      \
-                     workspace, workspace_bytes, s)
+                     workspace, workspace_bytes, q_rows, s)
     if (dtype == FLOUR_DTYPE_BF16) {
         if (out_dtype == FLOUR_DTYPE_F32) FLOUR_PF(bf16_t, float);
         if (out_dtype == FLOUR_DTYPE_BF16) FLOUR_PF(bf16_t, bf16_t);
@@ -1632,7 +1651,7 @@ extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stri
                                q_stride_head, k_pool, v_pool, cu_seqlens_q, kv_lens, block_tables,
                                max_blocks_per_seq, num_seqs, max_seqlen_q, total_q, num_heads,
                                kv_heads, head_dim, block_size, num_slots, scale, dtype, nullptr, 0,
-                               stream);
+                               nullptr, stream);
 }
 
 extern "C" int flour_hip_varlen_prefill_workspace_size(int num_seqs, int max_blocks_per_seq,
@@ -1678,5 +1697,32 @@ extern "C" int flour_hip_varlen_prefill_ws(void* out, int out_dtype, int64_t o_s
                                q_stride_head, k_pool, v_pool, cu_seqlens_q, kv_lens, block_tables,
                                max_blocks_per_seq, num_seqs, max_seqlen_q, total_q, num_heads,
                                kv_heads, head_dim, block_size, num_slots, scale, dtype, workspace,
-                               workspace_bytes, stream);
+                               workspace_bytes, nullptr, stream);
 }
+
+namespace flour {
+
+// Varlen prefill whose sequence s takes its q / out rows from row q_rows[s] on (its row count
+// still cu_seqlens_q[s + 1] - cu_seqlens_q[s]): the multi-row sequences of a mixed
+// continuous-batching step, whose packed rows sit among one-row sequences' rows. Matrix-core
+// shapes only (FLOUR_ERR_UNSUPPORTED otherwise, before any launch).
+int varlen_prefill_rows(void* out, int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,
+                        const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const void* k_pool, const void* v_pool, const int32_t* cu_seqlens_q,
+                        const int32_t* q_rows, const int32_t* kv_lens,
+                        const int32_t* block_tables, int max_blocks_per_seq, int num_seqs,
+                        int max_seqlen_q, int total_q, int num_heads, int kv_heads, int head_dim,
+                        int block_size, int64_t num_slots, float scale, int dtype,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+    if (!q_rows) {
+        set_error("varlen_prefill_rows: null row indices");
+        return FLOUR_ERR_INVALID_ARGUMENT;
+    }
+    return varlen_prefill_impl(out, out_dtype, o_stride_tok, o_stride_head, q, q_stride_tok,
+                               q_stride_head, k_pool, v_pool, cu_seqlens_q, kv_lens, block_tables,
+                               max_blocks_per_seq, num_seqs, max_seqlen_q, total_q, num_heads,
+                               kv_heads, head_dim, block_size, num_slots, scale, dtype, workspace,
+                               workspace_bytes, q_rows, stream);
+}
+
+}  // namespace flour

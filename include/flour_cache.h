@@ -216,7 +216,12 @@ int flour_kv_batch_rope_write_kv(flour_kv_batch* b, int layer, void* q_out, cons
                                  int64_t kv_stride_head, const void* cos_table,
                                  const void* sin_table, int max_pos, void* stream);
 /* Attention of the planned rows: paged decode when every sequence brings one row (q and out
- * (n_seqs, num_heads, head_dim) contiguous), varlen prefill otherwise (strided packed rows). */
+ * (n_seqs, num_heads, head_dim) contiguous), varlen prefill otherwise (strided packed rows).
+ * A mixed step (some sequences bring one row, others more) with packed contiguous q and out
+ * (row stride num_heads * head_dim, head stride head_dim) over 16-bit pools at head_dim 128
+ * runs its one-row sequences as one paged-decode launch and the others as one prefill launch,
+ * each over its rows of the packed layout; other mixed steps run every row on the prefill
+ * kernel. */
 int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void* q, int num_heads,
                              int64_t q_stride_tok, int64_t q_stride_head, void* out,
                              int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,

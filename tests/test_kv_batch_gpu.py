@@ -165,3 +165,84 @@ def test_rope_write_then_attention(device):
     with pytest.raises(_lib.FlourError, match="cover"):
         short_cos, short_sin = ops.rope_tables(512, D, 500000.0, torch.bfloat16, device)
         b.rope_write_kv(1, q, k, v, short_cos, short_sin)
+
+
+def _fill(b, sids, lens, layer, seed):
+    """Context rows for the listed sequences, written through planned steps (KV write only)."""
+    gd = torch.Generator(device="cuda").manual_seed(seed)
+    G_, D_ = b.kv_heads, b.head_dim
+    for i in range(0, len(sids), 8):
+        ids, ns = sids[i:i + 8], lens[i:i + 8]
+        b.step(ids, ns)
+        T = sum(ns)
+        k = torch.randn((T, G_, D_), generator=gd, device="cuda").to(b.dtype)
+        v = torch.randn((T, G_, D_), generator=gd, device="cuda").to(b.dtype)
+        b.write_kv(layer, k, v)
+
+
+def test_mixed_step_runs_decode_rows_on_the_decode_kernel(device):
+    """A continuous-batching step at the Llama-3-8B attention shape: 60 sequences decoding one
+    row each over contexts U[512, 4096] while 4 prompts of U[128, 512] rows prefill, listed
+    interleaved. The one-row sequences run as one paged-decode launch and the prompts as one
+    prefill launch, each over its rows of the packed layout: every row against the oracle,
+    the decode rows bit-identical to paged_decode over those sequences alone, the prompt rows
+    bit-identical to varlen_prefill over the prompts alone, and the all-prefill route (the
+    split switched off) against the oracle too."""
+    Hq, Gk, Dh = 32, 8, 128
+    rng = np.random.default_rng(41)
+    b = KvBatch(1, 10000, 64, 4096 + 16, 8 * 4096, Hq, Gk, Dh, torch.bfloat16, BS)
+    n_dec = 60
+    ctx = [int(x) for x in rng.integers(512, 4097, size=n_dec)]
+    prompts = [int(x) for x in rng.integers(128, 513, size=4)]
+    dec = [b.add_sequence() for _ in range(n_dec)]
+    _fill(b, dec, [c - 1 for c in ctx], 0, 5)
+    pro = [b.add_sequence() for _ in prompts]
+    order = dec[:5] + [pro[0]] + dec[5:20] + [pro[1]] + dec[20:33] + [pro[2]] + dec[33:] + [pro[3]]
+    qn = [prompts[pro.index(s)] if s in pro else 1 for s in order]
+    b.step(order, qn)
+    T = sum(qn)
+    gd = torch.Generator(device="cuda").manual_seed(6)
+    k = torch.randn((T, Gk, Dh), generator=gd, device="cuda").to(torch.bfloat16)
+    v = torch.randn((T, Gk, Dh), generator=gd, device="cuda").to(torch.bfloat16)
+    b.write_kv(0, k, v)
+    q = torch.randn((T, Hq, Dh), generator=gd, device="cuda").to(torch.bfloat16)
+    split = b.attention(0, q, SCALE, out_dtype=torch.float32)
+    assert _lib.lib().flour_hip_set_batch_split(0) == 0
+    try:
+        whole = b.attention(0, q, SCALE, out_dtype=torch.float32)
+    finally:
+        _lib.lib().flour_hip_set_batch_split(1)
+    torch.cuda.synchronize()
+
+    kp, vp = (to_np(t) for t in b.pool(0))
+    mb = max(len(b.blocks(s)) for s in order)
+    bt = np.zeros((len(order), mb), np.int32)
+    for i, s in enumerate(order):
+        bl = b.blocks(s)
+        bt[i, :len(bl)] = bl
+    cu = np.concatenate([[0], np.cumsum(qn)]).astype(np.int32)
+    kl = np.array([b.len(s) for s in order], np.int32)
+    ref = O.paged_attention(to_np(q), kp, vp, bt, cu, kl, BS, SCALE, bf16=True)
+    for tag, out in (("split", split), ("all-prefill", whole)):
+        max_abs, rel = errors(to_np(out), ref)
+        print(f"mixed step {tag}: max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+        assert max_abs <= 2e-3 and rel <= 1e-3
+
+    # the decode rows are the decode kernel's over the one-row sequences alone
+    di = [i for i, n in enumerate(qn) if n == 1]
+    d_rows = torch.tensor(cu[di], dtype=torch.long, device=device)
+    d_bt = torch.tensor(bt[di], device=device)
+    d_ctx = torch.tensor(kl[di], device=device)
+    alone = ops.paged_decode(q[d_rows].contiguous(), *b.pool(0), d_bt, d_ctx, SCALE,
+                             int(kl[di].max()), block_size=BS, out_dtype=torch.float32)
+    assert torch.equal(split[d_rows], alone)
+    # the prompt rows are the prefill kernel's over the prompts alone
+    pi = [i for i, n in enumerate(qn) if n > 1]
+    p_rows = torch.cat([torch.arange(cu[i], cu[i + 1]) for i in pi]).to(device)
+    p_cu = torch.tensor(np.concatenate([[0], np.cumsum([qn[i] for i in pi])]), dtype=torch.int32,
+                        device=device)
+    p_out = ops.varlen_prefill(q[p_rows].contiguous(), *b.pool(0), p_cu,
+                               torch.tensor(kl[pi], device=device),
+                               torch.tensor(bt[pi], device=device), max(qn), SCALE,
+                               block_size=BS, out_dtype=torch.float32)
+    assert torch.equal(split[p_rows], p_out)
