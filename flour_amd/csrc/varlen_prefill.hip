@@ -497,8 +497,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
             // first q / out row of the sequence: q_rows[seq] when given (the sequences of a
             // mixed step, whose rows sit among other sequences' rows), else its cu_seqlens start
-            const int q0 = q_rows ? q_rows[seq] : persistent ? sched_cu[seq] : cu_seqlens[seq];
-            const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - q0;
+            const int c0 = persistent ? sched_cu[seq] : cu_seqlens[seq];
+            const int q0 = q_rows ? q_rows[seq] : c0;
+            const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - c0;
             const int kvl = persistent ? sched_kv[seq] : min(kv_lens[seq], kv_cap);
             const int qt = NQ - 1 - level;
             const int row_last = min(qt * PF_QT + (256 >> lg), ql) - 1;  // the item's last row
