@@ -38,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+F32_PEAK_TFLOPS = 157.3        # MI355X dense fp32 matrix, TFLOP/s
 
 
 def parse_args():
@@ -440,8 +441,10 @@ def cpu_prefill_baseline(case, seconds: float):
     q, kp, vp = host(case.q), host(case.k_pool), host(case.v_pool)
     bt, cu, kl = host(case.block_tables), host(case.cu_seqlens_q), host(case.kv_lens)
     threads = O.num_threads()
+    f32 = case.q.dtype == torch.float32
     run = lambda: O.paged_attention(q, kp, vp, bt, cu, kl, case.block_size, case.scale,  # noqa: E731
-                                    out_dtype=np.uint16, threads=threads)
+                                    out_dtype=np.float32 if f32 else np.uint16,
+                                    bf16=case.q.dtype == torch.bfloat16, threads=threads)
     run()
     times = []
     t_end = time.perf_counter() + seconds
@@ -470,6 +473,15 @@ class _LazyNames(dict):
 DTYPE_NAME = _LazyNames()
 
 
+def prefill_kernel_name(case) -> str:
+    """The kernel a prefill workload runs on (the dispatch rule of flour_hip_varlen_prefill)."""
+    import torch
+
+    mfma = (case.q.dtype in (torch.bfloat16, torch.float16) and case.q.shape[2] in (64, 128)
+            and case.block_size % 16 == 0)
+    return "varlen_prefill_mfma_kernel" if mfma else "attn_simt_kernel"
+
+
 def decode_kernel_name(case) -> str:
     """Which kernel the library runs for a decode case (its dispatch rule, restated)."""
     import torch
@@ -480,6 +492,16 @@ def decode_kernel_name(case) -> str:
             case.block_size % 16 == 0 and H // G <= 16 and B <= 4096)
     return ("paged_decode_mfma_kernel + paged_decode_merge_kernel" if mfma
             else "attn_simt_kernel (vector ALUs)")
+
+
+def launch_floor_ms(torch, steps: int, warmup: int) -> float:
+    """ms per launch of an empty one-wave kernel, back to back on the current stream: the floor
+    under which no launch of this library can finish."""
+    from flour_amd import _lib
+    from flour_amd.ops import _stream
+
+    fn, st = _lib.lib().flour_hip_empty_launch, _stream()
+    return loop_timed(torch, lambda: fn(st), max(steps, 50), warmup)
 
 
 def bench_decode(torch, ops, case, steps, warmup, graph: bool = False):
@@ -527,7 +549,8 @@ def bench_decode(torch, ops, case, steps, warmup, graph: bool = False):
                 gbs_step=nbytes / (wall_ms * 1e-3) / 1e9, gbs_kernel=nbytes / (kern_ms * 1e-3) / 1e9)
 
 
-ROPE_THETA = {"prefill_bf16_varlen_llama3_8b": 500000.0, "prefill_bf16_prefix_qwen2_7b": 1000000.0}
+ROPE_THETA = {"prefill_bf16_varlen_llama3_8b": 500000.0, "prefill_bf16_prefix_qwen2_7b": 1000000.0,
+              "prefill_bf16_qwen25_05b": 1000000.0}
 
 
 def rope_inputs(torch, ops, case, theta):
@@ -602,21 +625,22 @@ def bench_prefill(torch, ops, case, steps, warmup, theta=500000.0):
 def prefill_line(torch, ops, case, name, cfg, args):
     """One JSON line for a prefill workload (KV write + causal varlen prefill per step)."""
     r = bench_prefill(torch, ops, case, args.steps, args.warmup, ROPE_THETA.get(name, 500000.0))
+    peak = F32_PEAK_TFLOPS if case.q.dtype == torch.float32 else BF16_PEAK_TFLOPS
     line = {
         "metric": "causal varlen prefill attention throughput (useful causal FLOPs)",
         "value": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(r["ms_per_step"], 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "scaling": "weak", "vs_baseline": None, "dtype": DTYPE_NAME[case.q.dtype],
         "data": "synthetic (seeded N(0,1); random slot mapping into a 1.25x pool)",
         "config": {"workload": name, "num_seqs": cfg["num_seqs"], "num_heads": cfg["num_heads"],
                    "kv_heads": cfg["kv_heads"], "head_dim": cfg["head_dim"],
                    "block_size": cfg["block_size"], "q_len": f"U[{cfg['q_len'][0]},{cfg['q_len'][1]}]",
                    "prefix": cfg["prefix"], "flops_per_step": r["flops"],
                    "input_copies": r["copies"]},
-        "roofline": {"bound": "mfma", "kernel": "varlen_prefill_mfma_kernel",
-                     "achieved": round(r["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": prefill_kernel_name(case),
+                     "achieved": round(r["tflops"], 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
                      "avg_launch_us": round(r["attn_ms"] * 1e3, 3), "traffic": read_traffic(name)},
         "kv_write": {"GB/s": round(r["write_gbs"], 1), "hbm_frac": round(r["write_gbs"] / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(r["write_ms"] * 1e3, 3), "bytes": r["write_bytes"],
@@ -755,6 +779,7 @@ def main():
                 e = {"GB/s": round(rr["gbs_kernel"], 1),
                      "hbm_frac": round(rr["gbs_kernel"] / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(rr["kernel_ms"] * 1e3, 2),
+                     "empty_launch_us": round(launch_floor_ms(torch, args.steps, args.warmup) * 1e3, 2),
                      "algorithmic_bytes": rr["bytes"],
                      "traffic": read_traffic(nm),
                      "kernel": decode_kernel_name(cs)}
@@ -766,8 +791,10 @@ def main():
                 extra[nm] = e
             else:
                 rr = bench_prefill(torch, ops, cs, args.steps, args.warmup, ROPE_THETA.get(nm, 500000.0))
+                peak = F32_PEAK_TFLOPS if cs.q.dtype == torch.float32 else BF16_PEAK_TFLOPS
                 e = {"TFLOP/s": round(rr["tflops"], 1),
-                     "mfma_frac": round(rr["tflops"] / BF16_PEAK_TFLOPS, 4),
+                     "mfma_frac": round(rr["tflops"] / peak, 4), "peak_TFLOP/s": peak,
+                     "kernel": prefill_kernel_name(cs),
                      "attn_us": round(rr["attn_ms"] * 1e3, 2), "flops": rr["flops"],
                      "traffic": read_traffic(nm),
                      "kv_write_traffic": read_traffic(nm.replace("prefill_", "kv_write_")),

@@ -160,6 +160,7 @@ EXTRA_SIGNATURES: dict[str, tuple] = {
     "flour_hip_set_prefill_persistent": (_c_int, [_c_int]),
     "flour_hip_set_prefill_dma": (_c_int, [_c_int]),
     "flour_hip_set_batch_split": (_c_int, [_c_int]),
+    "flour_hip_empty_launch": (_c_int, [_vp]),
 }
 
 

@@ -204,7 +204,16 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
     // ---- chunks of waves * RPL * SIMT_UNROLL rows: row j = c0 + (u * waves + w) * RPL + grp.
     // The next chunk's rows are loaded while this one is computed.
     const int chunk = waves * RPL * SIMT_UNROLL;
+    // The block id of row j is read whether or not j < kv_end (the index is clamped into the
+    // table row), so that it does not wait for the kv length: a step's K/V loads then depend on
+    // one memory round trip (its block ids), not two.
     auto load = [&](int c0, u32x4* kr, u32x4* vr, int* jr) __attribute__((always_inline)) {
+        int64_t ids[SIMT_UNROLL];
+#pragma unroll
+        for (int u = 0; u < SIMT_UNROLL; u++) {
+            const int j = c0 + (u * waves + w) * RPL + grp;
+            ids[u] = bt[min(j / block_size, max_blocks - 1)];
+        }
 #pragma unroll
         for (int u = 0; u < SIMT_UNROLL; u++) {
             const int j = c0 + (u * waves + w) * RPL + grp;
@@ -212,8 +221,8 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
             int64_t row = 0;  // rows past the end read row 0 of the pool (their scores are masked)
             if (j < kv_end) {
                 const int lb = j / block_size;
-                int64_t phys = bt[lb];  // clamped: a bad block id never leaves the pool
-                phys = phys < 0 ? 0 : (phys > max_phys ? max_phys : phys);
+                // clamped: a bad block id never leaves the pool
+                const int64_t phys = ids[u] < 0 ? 0 : (ids[u] > max_phys ? max_phys : ids[u]);
                 row = (phys * block_size + (j - lb * block_size)) * head_dim;
             }
             kr[u] = *reinterpret_cast<const u32x4*>(kbase + row);
@@ -264,7 +273,7 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
             }
         }
     };
-    if (kv_end > 0) load(0, ka, va, ja);
+    load(0, ka, va, ja);  // unconditional, so that it need not wait for the kv length
     for (int c0 = 0; c0 < kv_end; c0 += 2 * chunk) {
         const bool more = c0 + chunk < kv_end;
         if (more) load(c0 + chunk, kb, vb, jb);

@@ -676,6 +676,17 @@ static int launch_decode_mfma(int head_dim, void* out, const void* q, const void
 
 using namespace flour;
 
+namespace flour {
+__global__ void empty_kernel() {}
+}  // namespace flour
+
+// One empty one-wave workgroup on `stream`: the floor of a kernel launch on this device, timed
+// beside the smallest decode workloads (a measurement helper, not part of the header).
+extern "C" int flour_hip_empty_launch(void* stream) {
+    flour::empty_kernel<<<dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream)>>>();
+    return check_hip(hipGetLastError(), "empty launch");
+}
+
 extern "C" int flour_hip_set_decode_workgroups(int n) {
     if (n < 0 || n > 4096) return FLOUR_ERR_INVALID_ARGUMENT;
     g_wg_override = n;

@@ -61,17 +61,21 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
                         int num_heads, int n_rep, int head_dim, int block_size, int64_t num_slots,
                         int max_kv, float scale, hipStream_t stream);
 
-static constexpr int PF_D = 128;
+static constexpr int PF_D = 128;   // head dims of the matrix-core path: 128 and PF_D64
+static constexpr int PF_D64 = 64;
 static constexpr int PF_QT = 128;  // query rows per head per workgroup (4 waves x 32)
 static constexpr int PF_KT = 64;   // kv tokens per tile
 static constexpr int PF_WAVES = 8; // two query heads of one kv head x 4 waves
 static constexpr int PF_THREADS = PF_WAVES * 64;
 static constexpr float PF_RESCALE_SLACK = 8.0f;  // log2 units the reference max may lag
-static constexpr int PF_KPITCH = PF_D + 8;   // elements: 272 B rows
+// K rows in LDS (register staging): head_dim + 8 elements, 272 B at 128 and 144 B at 64
+__host__ __device__ constexpr int pf_kpitch(int d) { return d + 8; }
 static constexpr int PF_VPITCH = PF_KT + 8;  // elements: 144 B rows
 static constexpr int PF_OPITCH = 68;         // elements: 136 B rows of output staging
-static_assert(4 * 32 * PF_OPITCH <= PF_KT * PF_KPITCH && 4 * 32 * PF_OPITCH <= PF_D * PF_VPITCH,
-              "output staging fits one K / V buffer per head");
+// Per-wave Q staging block (register staging): 32 rows of up to 128 dims, 8 KB; it also
+// stages the output, 32 rows of 64 dims at a time with the PF_OPITCH pitch.
+static constexpr int PF_QSTAGE_ELEMS = 32 * PF_D;
+static_assert(32 * PF_OPITCH <= PF_QSTAGE_ELEMS, "output staging fits a wave's Q block");
 static constexpr float PF_LOG2E = 1.4426950408889634f;
 // Persistent schedule limits (the per-workgroup item table lives in LDS); larger batches use
 // one workgroup per item.
@@ -111,26 +115,28 @@ enum { PV_F16 = 0, PV_HILO = 1 };
 
 static constexpr uint32_t PF_OOR = 0x80000000u;  // buffer offset past any pool: loads read 0
 
-// Direct-to-LDS staging (the DMA kernel): three LDS tile buffers; V comes pre-widened from a
-// staging copy of 4 KB pages, each 16 tokens of one kv head as V^T (128 dims x 16 fp16, token
-// sigma16(k) at position k), written by prefill_v_stage_kernel before the attention launch.
+// Direct-to-LDS staging (the DMA kernel, head_dim 128): three LDS tile buffers; V comes
+// pre-widened from a staging copy of 4 KB pages, each 16 tokens of one kv head as V^T (128 dims
+// x 16 fp16, token sigma16(k) at position k), written by prefill_v_stage_kernel before the
+// attention launch.
 static constexpr int PF_VPAGE_BYTES = 16 * PF_D * 2;
 
 // 64 lanes x 16 bytes from a raw buffer straight into LDS: lane L's bytes come from
 // rsrc.base + soff + voff and land at LDS byte lds + 16 L; lanes past the buffer's size write
 // zeros. Issued from inline asm so that the compiler's wait-count tracking, which knows nothing
 // of these loads, adds no waits for them to the LDS reads; every wait for them is explicit.
-// M0 (the LDS destination) is written here; "m0" in the clobber list makes the compiler keep
-// no live value of its own in M0 across the statement. The s_nop 0 between the M0 write and the
-// load is the wait state a vector memory instruction that reads M0 needs after an SALU write of
-// M0 (the hardware does not interlock it, and the compiler's hazard tracking does not look
-// inside inline asm).
+// M0 (the LDS destination) is written here. The AMDGPU backend treats M0 as a reserved
+// register and ignores it in clobber lists; none of its own code in these kernels reads M0 (the
+// generated ISA has no M0 reader other than these loads), so no compiler value can be
+// overwritten. The s_nop 0 between the M0 write and the load is the wait state a vector memory
+// instruction that reads M0 needs after an SALU write of M0 (the hardware does not interlock
+// it, and the compiler's hazard tracking does not look inside inline asm).
 __device__ __forceinline__ void dma_b128(uint32_t voff, __amdgpu_buffer_rsrc_t rsrc, uint32_t lds,
                                          uint32_t soff) {
     const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
     const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
-                 :: "v"(voff), "s"(rsrc), "s"(l), "s"(so) : "memory", "m0");
+                 :: "v"(voff), "s"(rsrc), "s"(l), "s"(so) : "memory");
 }
 // 16-byte global store issued from inline asm: the compiler's wait-count tracking does not see
 // it, so pending output stores never turn its waits for tile loads into full drains (loads and
@@ -149,7 +155,7 @@ __device__ __forceinline__ int sigma16(int t) {  // swap bits 2 and 3 (token ord
     return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1);
 }
 
-template <typename T, typename TO, int PV, bool BS16, bool DMA>
+template <typename T, typename TO, int PV, bool BS16, bool DMA, int D>
 __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     TO* __restrict__ out, int64_t o_st, int64_t o_sh, const T* __restrict__ q, int64_t q_st,
     int64_t q_sh, const T* __restrict__ k_pool, const T* __restrict__ v_pool,
@@ -161,7 +167,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // DMA: K and V tiles go straight from memory into LDS (K from the pool, V from the staging
     // copy), three buffers, no staging registers. It needs the persistent schedule and fp16 P.V.
     static_assert(!DMA || PV == PV_F16, "the DMA kernel runs the fp16 P.V path");
-    constexpr int D = PF_D;
+    static_assert(!DMA || D == PF_D, "the DMA kernel runs head_dim 128");
+    static_assert(D == PF_D || D == PF_D64, "matrix-core prefill: head_dim 128 or 64");
+    constexpr int KPITCH = pf_kpitch(D);
+    constexpr int CPR = D / 8;         // 16-byte chunks per K / V row
+    constexpr int NKQ = D / 16;        // 16-dim k-steps of S^T = K Q^T (Q^T registers)
+    constexpr int NMT = D / 32;        // 32-dim blocks of O^T = V^T P^T
     // V^T is staged as fp16 for PV_F16, as the storage type otherwise; K keeps the storage type.
     typedef typename std::conditional<PV == PV_F16, f16_t, T>::type TV;
     // bf16 V is widened to fp16 scaled by 2^8 and each item's output blocks are checked at its
@@ -173,8 +184,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     //    c ^ (r % 16) (conflict-free fragment reads); V^T as four 4 KB pages (the staging copy's
     //    layout), or in exact mode the register-staged V^T with a 144 B pitch; three buffers.
     constexpr int NBUF = DMA ? 3 : 2;
-    constexpr int K_ELEMS = DMA ? PF_KT * PF_D : PF_KT * PF_KPITCH;
-    constexpr int TILE_ELEMS = K_ELEMS + PF_D * PF_VPITCH;
+    constexpr int K_ELEMS = DMA ? PF_KT * D : PF_KT * KPITCH;
+    constexpr int TILE_ELEMS = K_ELEMS + D * PF_VPITCH;
     static_assert(!DMA || 8 * 32 * PF_OPITCH <= TILE_ELEMS, "output staging fits one buffer");
     __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF * TILE_ELEMS];
     auto kb_ptr = [&](int b) { return &tiles[b * TILE_ELEMS]; };
@@ -216,7 +227,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     constexpr bool FLEX = !DMA;
     constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1 +
                                (FLEX ? 2 * (PF_FLEX_ENTRIES + 1) : 0);
-    constexpr int QSTAGE_BYTES = DMA ? 0 : PF_WAVES * 32 * PF_D * 2;
+    constexpr int QSTAGE_BYTES = DMA ? 0 : PF_WAVES * PF_QSTAGE_ELEMS * 2;
     constexpr int SCHED_BYTES = 4 * SCHED_INTS > QSTAGE_BYTES ? 4 * SCHED_INTS : QSTAGE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t sched_raw[SCHED_BYTES];
     int* const sched_order = reinterpret_cast<int*>(sched_raw);  // sequences by decreasing tile count
@@ -557,13 +568,19 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
 
     // ---- staging assignment (a 64-token tile is four 16-token groups, each inside one page)
-    // K: two 16 B chunks per thread: token (tid / 16) + 32i of the tile, dims (tid % 16) * 8;
-    //    the group of each chunk, (tid / 256) + 2i, is the same for the whole wave.
-    // V: token pair tp = tid % 32 (tokens 2tp, 2tp+1), dims 8dg..8dg+7 with dg = tid / 32;
-    //    stored transposed, token t at column sigma16(t). Its group tp / 8 varies per lane.
-    const int k_row = tid >> 4, k_col = (tid & 15) * 8;
+    // K: KPASS 16 B chunks per thread: token (tid / CPR) + RPP i of the tile, dims
+    //    (tid % CPR) * 8 (head_dim 128: two chunks, rows tid / 16 and + 32; head_dim 64: one,
+    //    row tid / 8); the group of each chunk, k_grp + (RPP / 16) i, is the same for the whole
+    //    wave.
+    // V: token pair tp = tid % 32 (tokens 2tp, 2tp+1), dims 8dg..8dg+7 with dg = tid / 32 (at
+    //    head_dim 64 only waves 0-3, dg < 8, stage V); stored transposed, token t at column
+    //    sigma16(t). Its group tp / 8 varies per lane.
+    constexpr int RPP = PF_THREADS / CPR;  // K rows per staging pass
+    constexpr int KPASS = PF_KT / RPP;
+    const int k_row = tid / CPR, k_col = (tid % CPR) * 8;
     const int v_tp = tid & 31, v_dg = tid >> 5;
-    const int k_grp = w >> 2;
+    const bool v_on = D == PF_D || v_dg < CPR;  // wave-uniform
+    const int k_grp = (64 / CPR) * w / 16;
     constexpr uint32_t ROW_BYTES = D * sizeof(T);
     const uint32_t k_lane = (uint32_t)((k_row & 15) * D + k_col) * (uint32_t)sizeof(T);
     const uint32_t v_lane = (uint32_t)((2 * v_tp & 15) * D + 8 * v_dg) * (uint32_t)sizeof(T);
@@ -653,7 +670,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // Branch-free tile loads into (kd, vd): tokens past kv_len (or a tile past the last) get an
     // out-of-range offset and read zeros.
     auto gload_v = [&](int kt, const int* pb, bool valid, u32x4* vd) {
-        const int lim_rel = (valid ? kv_len : 0) - kt * PF_KT;  // tile tokens t < lim_rel exist
+        // tile tokens t < lim_rel exist (none for the waves without V staging)
+        const int lim_rel = (valid && v_on ? kv_len : 0) - kt * PF_KT;
         const int b01 = v_g1 ? pb[1] : pb[0], b23 = v_g1 ? pb[3] : pb[2];
         const uint32_t vb = (uint32_t)(v_g2 ? b23 : b01) + v_lane;
 #pragma unroll
@@ -665,17 +683,24 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     auto gload_to = [&](__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs, int lim_rel,
                         const int* pb, u32x4* kd, u32x4* vd) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t o = (uint32_t)(k_grp ? pb[2 * i + 1] : pb[2 * i]) + k_lane;
+        for (int i = 0; i < KPASS; i++) {
+            int kpb;
+            if constexpr (D == PF_D) {
+                kpb = k_grp ? pb[2 * i + 1] : pb[2 * i];
+            } else {
+                kpb = k_grp == 0 ? pb[0] : k_grp == 1 ? pb[1] : k_grp == 2 ? pb[2] : pb[3];
+            }
+            const uint32_t o = (uint32_t)kpb + k_lane;
             kd[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                krs, k_row + 32 * i < lim_rel ? o : PF_OOR, 0, 0);
+                krs, k_row + RPP * i < lim_rel ? o : PF_OOR, 0, 0);
         }
         const int b01 = v_g1 ? pb[1] : pb[0], b23 = v_g1 ? pb[3] : pb[2];
         const uint32_t vb = (uint32_t)(v_g2 ? b23 : b01) + v_lane;
+        const int vlim = v_on ? lim_rel : 0;
 #pragma unroll
         for (int j = 0; j < 2; j++)
             vd[j] = __builtin_amdgcn_raw_buffer_load_b128(
-                vrs, 2 * v_tp + j < lim_rel ? vb + j * ROW_BYTES : PF_OOR, 0, BUF_NT);
+                vrs, 2 * v_tp + j < vlim ? vb + j * ROW_BYTES : PF_OOR, 0, BUF_NT);
     };
     auto gload = [&](int kt, const int* pb, bool valid, u32x4* kd, u32x4* vd) {
         gload_to(k_rsrc, v_rsrc, (valid ? kv_len : 0) - kt * PF_KT, pb, kd, vd);
@@ -721,6 +746,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
     // `ex` true: exact mode, V is stored as bf16 without widening
     auto lds_store_v = [&](auto ex, int buf, u32x4* vd) {
+        if (!v_on) return;  // head_dim 64: waves 4-7 stage no V
         if constexpr (CHECK_V && !decltype(ex)::value) {
             // widen bf16 V to fp16 as v * 2^8 (exact for 2^-25 <= |v| <= 255 and 0)
 #pragma unroll
@@ -740,8 +766,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
     auto lds_store = [&](auto ex, int buf, u32x4* kd, u32x4* vd) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-            *reinterpret_cast<u32x4*>(&kb_ptr(buf)[(k_row + 32 * i) * PF_KPITCH + k_col]) = kd[i];
+        for (int i = 0; i < KPASS; i++)
+            *reinterpret_cast<u32x4*>(&kb_ptr(buf)[(k_row + RPP * i) * KPITCH + k_col]) = kd[i];
         lds_store_v(ex, buf, vd);
     };
 
@@ -762,19 +788,19 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
     // Q^T as the B operand: lane (h2, q) holds row q, dims 16kk + 8h2 .. +7 (idle waves and
     // padded rows read a valid row)
-    u32x4 qb[8];
+    u32x4 qb[NKQ];
     auto load_q = [&](const Item& it) __attribute__((always_inline)) {
         const int hq = it.kvh * n_rep + min(wave_hl(it), n_rep - 1);
         const int row = min(it.qt * PF_QT + 32 * wave_rb(it) + ql32, it.ql - 1);
         const T* qp = q + (int64_t)(it.q0 + row) * q_st + (int64_t)hq * q_sh + 8 * h2;
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++) qb[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
+        for (int kk = 0; kk < NKQ; kk++) qb[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
     };
     // Register staging: an item's Q rows reach this wave's staging block straight from memory
-    // (eight 1 KB loads issued an item ahead, no registers held), then qb comes from LDS. Lane
-    // (r4, c) = (lane / 16, lane % 16) of load i reads chunk c ^ r of row r = 4i + r4, clamped
-    // to the sequence's last row like load_q.
-    uint16_t* const qstage = reinterpret_cast<uint16_t*>(sched_raw) + w * (32 * PF_D);
+    // (D / 16 loads of 1 KB issued an item ahead, no registers held), then qb comes from LDS.
+    // Lane (r, c) = (lane / CPR, lane % CPR) of load i reads chunk c ^ (row % CPR) of row
+    // (64 / CPR) i + r, clamped to the sequence's last row like load_q.
+    uint16_t* const qstage = reinterpret_cast<uint16_t*>(sched_raw) + w * PF_QSTAGE_ELEMS;
     auto dma_q = [&](const Item& it) __attribute__((always_inline)) {
         const int hq = it.kvh * n_rep + min(wave_hl(it), n_rep - 1);
         const int row0 = it.qt * PF_QT + 32 * wave_rb(it);
@@ -784,32 +810,32 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             __builtin_amdgcn_make_buffer_rsrc((void*)qp, (short)0, (int)0x7fffffff, BUF_DWORD3);
         const uint32_t qs = lds_byte_addr(qstage);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int r = 4 * i + (lane >> 4);
+        for (int i = 0; i < NKQ; i++) {
+            const int r = (64 / CPR) * i + lane / CPR;
             const int row = min(row0 + r, it.ql - 1) - rb;
             const uint32_t off = (uint32_t)row * (uint32_t)(q_st * (int64_t)sizeof(T)) +
-                                 (uint32_t)(((lane & 15) ^ (r & 15)) * 16);
+                                 (uint32_t)(((lane % CPR) ^ (r % CPR)) * 16);
             dma_b128(off, q_rsrc, qs + 1024u * i, 0u);
         }
     };
     // qb from the staging block (the loads that filled it must be complete)
     auto read_q = [&]() __attribute__((always_inline)) {
-        const uint16_t* qr = qstage + ql32 * PF_D;
+        const uint16_t* qr = qstage + ql32 * D;
 #pragma unroll
-        for (int kk = 0; kk < 8; kk++)
-            qb[kk] = *reinterpret_cast<const u32x4*>(qr + 8 * ((2 * kk + h2) ^ (ql32 & 15)));
+        for (int kk = 0; kk < NKQ; kk++)
+            qb[kk] = *reinterpret_cast<const u32x4*>(qr + 8 * ((2 * kk + h2) ^ (ql32 % CPR)));
     };
 
     float out_scale = 1.0f;  // 2^-8 after the fp16 path over bf16 V (CHECK_V), else 1
     // Running state: the reference max m may lag the true running max by up to
     // PF_RESCALE_SLACK (weights then reach 2^8), which skips most accumulator rescales.
     float m = -INFINITY, lsum = 0.0f;
-    f32x16 o[4];
+    f32x16 o[NMT];
     auto reset_state = [&]() {
         m = -INFINITY;
         lsum = 0.0f;
 #pragma unroll
-        for (int x = 0; x < 4; x++)
+        for (int x = 0; x < NMT; x++)
 #pragma unroll
             for (int y = 0; y < 16; y++) o[x][y] = 0.0f;
     };
@@ -824,7 +850,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 if (orow < ql) {
                     TO* op = out + (int64_t)(q0 + orow) * o_st + (int64_t)head * o_sh + 4 * h2;
 #pragma unroll
-                    for (int mt2 = 0; mt2 < 4; mt2++)
+                    for (int mt2 = 0; mt2 < NMT; mt2++)
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
                             const f32x4 v = f32x4{o[mt2][4 * i] * inv, o[mt2][4 * i + 1] * inv,
@@ -838,14 +864,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             } else {
                 // 16-bit output goes through LDS (DMA: tile buffer sbuf, idle until a barrier
                 // that comes before its next fill; register staging: this wave's Q staging
-                // block, whose rows are in qb by now) in two 64-dim halves, so that each store
+                // block, whose rows are in qb by now) in 64-dim halves, so that each store
                 // writes whole 128 B row segments: lane (r, c) = (lane / 8, lane % 8) stores
                 // dims 8c .. 8c + 7 of rows r, r + 8, r + 16, r + 24.
                 uint16_t* stg = DMA ? kb_ptr(sbuf) + w * (32 * PF_OPITCH) : qstage;
                 const int rr = lane >> 3, cc = lane & 7;
                 TO* ob = out + (int64_t)(q0 + wr0) * o_st + (int64_t)head * o_sh + 8 * cc;
 #pragma unroll
-                for (int half = 0; half < 2; half++) {
+                for (int half = 0; half < D / 64; half++) {
 #pragma unroll
                     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -890,18 +916,19 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // read four products ahead. `fill` is work independent of the scores (the staging of the
     // next tile) that the products are interleaved with.
     auto qk = [&](int kbuf, auto&& fill) __attribute__((always_inline)) {
-        const uint16_t* kr = DMA ? kb_ptr(kbuf) + ql32 * PF_D : kb_ptr(kbuf) + ql32 * PF_KPITCH + 8 * h2;
+        const uint16_t* kr = DMA ? kb_ptr(kbuf) + ql32 * D : kb_ptr(kbuf) + ql32 * KPITCH + 8 * h2;
         auto frag = [&](int i) {  // product i: half i & 1, dims 16 (i >> 1) .. of the K rows
             if constexpr (DMA) {
                 // 16-byte chunk 2 (i >> 1) + h2 of row ql32 + 32 (i & 1), stored at chunk
                 // (2 (i >> 1) + h2) ^ (ql32 % 16)
                 return *reinterpret_cast<const u32x4*>(
-                    kr + (i & 1) * 32 * PF_D + 8 * ((2 * (i >> 1) + h2) ^ (ql32 & 15)));
+                    kr + (i & 1) * 32 * D + 8 * ((2 * (i >> 1) + h2) ^ (ql32 & 15)));
             } else {
-                return *reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * PF_KPITCH + 16 * (i >> 1));
+                return *reinterpret_cast<const u32x4*>(kr + (i & 1) * 32 * KPITCH + 16 * (i >> 1));
             }
         };
-        u32x4 fr[16];
+        constexpr int NP = 2 * NKQ;  // products: two 32-token halves x the k-steps
+        u32x4 fr[NP];
 #pragma unroll
         for (int i = 0; i < 4; i++) fr[i] = frag(i);
 #pragma unroll
@@ -915,12 +942,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         __builtin_amdgcn_s_setprio(1);
         fill();
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            if (i + 4 < 16) fr[i + 4] = frag(i + 4);
+        for (int i = 0; i < NP; i++) {
+            if (i + 4 < NP) fr[i + 4] = frag(i + 4);
             st[i & 1] = mfma32x32x16<T>(fr[i], qb[i >> 1], st[i & 1]);
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
+        for (int i = 0; i < NP; i++) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a K fragment read
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
             __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to three VALU
@@ -969,7 +996,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             const float alpha = fast_exp2(m - m_new);
             lsum *= alpha;
 #pragma unroll
-            for (int x = 0; x < 4; x++) o[x] *= alpha;
+            for (int x = 0; x < NMT; x++) o[x] *= alpha;
             m = m_new;
         }
     };
@@ -999,18 +1026,18 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
         };
         // Issue order, pinned with scheduling fences: the V reads and weights of step 0, then
-        // each product of step kk2 followed by one V read and a quarter of the weights of
-        // step kk2 + 1.
+        // each product of step kk2 followed by one V read and its share of the weights of
+        // step kk2 + 1 (a quarter at head_dim 128, a half at 64).
         // V^T fragment (dims 32 mt2 + ql32, tokens 8 h2 .. of group kk2): register staging keeps
         // V^T rows with a 144 B pitch; the DMA path has four 4 KB pages (128 dims x 16 tokens)
         const uint16_t* vr = DMA ? vb_ptr(vbuf) + ql32 * 16 + 8 * h2 : vb_ptr(vbuf) + ql32 * PF_VPITCH + 8 * h2;
         auto vfrag = [&](int mt2, int kk2) {
             return *reinterpret_cast<const u32x4*>(
-                DMA ? vr + kk2 * (16 * PF_D) + mt2 * 512 : vr + 32 * mt2 * PF_VPITCH + 16 * kk2);
+                DMA ? vr + kk2 * (16 * D) + mt2 * 512 : vr + 32 * mt2 * PF_VPITCH + 16 * kk2);
         };
-        u32x4 vf[2][4];
+        u32x4 vf[2][NMT];
 #pragma unroll
-        for (int mt2 = 0; mt2 < 4; mt2++) vf[0][mt2] = vfrag(mt2, 0);
+        for (int mt2 = 0; mt2 < NMT; mt2++) vf[0][mt2] = vfrag(mt2, 0);
 #pragma unroll
         for (int x = 0; x < 4; x++) weight(0, x);
         __builtin_amdgcn_sched_barrier(0);
@@ -1018,13 +1045,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 #pragma unroll
         for (int kk2 = 0; kk2 < 4; kk2++) {
 #pragma unroll
-            for (int mt2 = 0; mt2 < 4; mt2++) {
+            for (int mt2 = 0; mt2 < NMT; mt2++) {
                 o[mt2] = mfma32x32x16<TV>(vf[kk2 & 1][mt2], pb_hi[kk2], o[mt2]);
                 if constexpr (PV == PV_HILO)
                     o[mt2] = mfma32x32x16<TV>(vf[kk2 & 1][mt2], pb_lo[kk2], o[mt2]);
                 if (kk2 < 3) {
                     vf[(kk2 + 1) & 1][mt2] = vfrag(mt2, kk2 + 1);
-                    weight(kk2 + 1, mt2);
+#pragma unroll
+                    for (int x = mt2 * (4 / NMT); x < (mt2 + 1) * (4 / NMT); x++) weight(kk2 + 1, x);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -1053,7 +1081,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 psum += a0 + a1;
             }
 #pragma unroll
-            for (int mt2 = 0; mt2 < 4; mt2++) {
+            for (int mt2 = 0; mt2 < NMT; mt2++) {
                 const u32x4 vv = *reinterpret_cast<const u32x4*>(vr + 32 * mt2 * PF_VPITCH + 16 * kk2);
                 o[mt2] = mfma32x32x16<T>(vv, ph, o[mt2]);
                 o[mt2] = mfma32x32x16<T>(vv, pl, o[mt2]);
@@ -1141,7 +1169,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     auto block_untrusted = [&]() __attribute__((always_inline)) {
         float mx = 0.0f;
 #pragma unroll
-        for (int x = 0; x < 4; x++)
+        for (int x = 0; x < NMT; x++)
 #pragma unroll
             for (int y = 0; y < 16; y += 2)
                 mx = vmax(vmax(mx, __builtin_fabsf(o[x][y])), __builtin_fabsf(o[x][y + 1]));
@@ -1463,7 +1491,7 @@ static int64_t prefill_stage_bytes(int64_t num_seqs, int64_t max_blocks, int64_t
     return bytes <= PF_STAGE_MAX_BYTES ? bytes : 0;
 }
 
-template <typename T, typename TO, int PV>
+template <typename T, typename TO, int PV, int D>
 static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void* q,
                                int64_t q_st, int64_t q_sh, const void* k_pool, const void* v_pool,
                                const int32_t* cu, const int32_t* kv_lens, const int32_t* bt,
@@ -1482,7 +1510,7 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
         return FLOUR_ERR_UNSUPPORTED;
     }
     if (grid == 0) return FLOUR_OK;
-    if constexpr (PV == PV_F16) {
+    if constexpr (PV == PV_F16 && D == PF_D) {
         // DMA path: the V staging copy lives in the caller's workspace; two launches, the
         // staging pre-pass then the attention kernel.
         const int kv_heads = num_heads / n_rep;
@@ -1498,8 +1526,8 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
                 kv_heads, block_size, num_slots, (int)pages_per_seq);
             const int rc = check_hip(hipGetLastError(), "varlen_prefill V staging launch");
             if (rc != FLOUR_OK) return rc;
-            auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, true>
-                                         : varlen_prefill_mfma_kernel<T, TO, PV, false, true>;
+            auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, true, D>
+                                         : varlen_prefill_mfma_kernel<T, TO, PV, false, true, D>;
             kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
                 static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
                 static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt,
@@ -1509,8 +1537,8 @@ static int launch_prefill_mfma(void* out, int64_t o_st, int64_t o_sh, const void
             return check_hip(hipGetLastError(), "varlen_prefill launch");
         }
     }
-    auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, false>
-                                 : varlen_prefill_mfma_kernel<T, TO, PV, false, false>;
+    auto kern = block_size == 16 ? varlen_prefill_mfma_kernel<T, TO, PV, true, false, D>
+                                 : varlen_prefill_mfma_kernel<T, TO, PV, false, false, D>;
     kern<<<dim3((unsigned)grid), dim3(PF_THREADS), 0, stream>>>(
         static_cast<TO*>(out), o_st, o_sh, static_cast<const T*>(q), q_st, q_sh,
         static_cast<const T*>(k_pool), static_cast<const T*>(v_pool), cu, kv_lens, bt, max_blocks,
@@ -1552,8 +1580,8 @@ namespace flour {
 bool prefill_mfma_supported(int dtype, int head_dim, int block_size, int64_t num_slots,
                             float scale, int64_t q_stride_tok) {
     // (the Q rows of a wave are loaded with 32-bit offsets from its first row: 31 row strides)
-    return (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) && head_dim == PF_D &&
-           block_size % 16 == 0 && num_slots % block_size == 0 && scale > 0.0f &&
+    return (dtype == FLOUR_DTYPE_BF16 || dtype == FLOUR_DTYPE_F16) &&
+           (head_dim == PF_D || head_dim == PF_D64) && block_size % 16 == 0 && num_slots % block_size == 0 && scale > 0.0f &&
            num_slots * head_dim * 2 <= (int64_t)0x7fffffff && q_stride_tok >= 0 &&
            q_stride_tok * 2 * 32 <= (int64_t)0x7fffffff;
 }
@@ -1616,18 +1644,23 @@ static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
                                    num_heads, n_rep, head_dim, block_size, num_slots, INT_MAX,
                                    scale, s);
     }
-#define FLOUR_PF(T, TO)                                                                          \
+#define FLOUR_PF_D(T, TO, D)                                                                     \
     return g_prefill_pv_mode == PV_HILO                                                          \
-               ? launch_prefill_mfma<T, TO, PV_HILO>(                                            \
+               ? launch_prefill_mfma<T, TO, PV_HILO, D>(                                         \
                      out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
                      v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
                      max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale,      \
                      workspace, workspace_bytes, q_rows, s)                                      \
-               : launch_prefill_mfma<T, TO, PV_F16>(                                             \
+               : launch_prefill_mfma<T, TO, PV_F16, D>(                                          \
                      out, o_stride_tok, o_stride_head, q, q_stride_tok, q_stride_head, k_pool,   \
                      v_pool, cu_seqlens_q, kv_lens, block_tables, max_blocks_per_seq, num_seqs,  \
                      max_seqlen_q, total_q, num_heads, n_rep, block_size, num_slots, scale,      \
                      workspace, workspace_bytes, q_rows, s)
+#define FLOUR_PF(T, TO)                                                                          \
+    do {                                                                                         \
+        if (head_dim == PF_D64) FLOUR_PF_D(T, TO, PF_D64);                                       \
+        FLOUR_PF_D(T, TO, PF_D);                                                                 \
+    } while (0)
     if (dtype == FLOUR_DTYPE_BF16) {
         if (out_dtype == FLOUR_DTYPE_F32) FLOUR_PF(bf16_t, float);
         if (out_dtype == FLOUR_DTYPE_BF16) FLOUR_PF(bf16_t, bf16_t);
@@ -1637,6 +1670,7 @@ static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
     if (out_dtype == FLOUR_DTYPE_BF16) FLOUR_PF(f16_t, bf16_t);
     FLOUR_PF(f16_t, f16_t);
 #undef FLOUR_PF
+#undef FLOUR_PF_D
 }
 
 extern "C" int flour_hip_varlen_prefill(void* out, int out_dtype, int64_t o_stride_tok,

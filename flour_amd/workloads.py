@@ -19,6 +19,12 @@ N(0, 1) unless stated):
                                 context U[16384, 32768]
   decode_bf16_qwen25_05b        bf16 decode at head_dim 64 (the Qwen2.5-0.5B-Instruct attention
                                 shape): batch 64, 14 q / 2 kv heads, context U[512, 4096]
+  prefill_bf16_qwen25_05b       KV write + causal varlen prefill at head_dim 64 (Qwen2.5-0.5B:
+                                14 q / 2 kv heads), 8 prompts of U[256, 1024] tokens (the
+                                reference's load test sends prompts of up to 1,024 tokens)
+  prefill_f32_h8_d64            KV write + causal varlen prefill in fp32 (the reference's model
+                                dtype when config.json names none): 4 sequences of U[128, 512]
+                                tokens, 8 q / 8 kv heads, head_dim 64
 
 Physical blocks are a seeded random permutation of a pool 1.25x the blocks needed.
 """
@@ -51,6 +57,12 @@ WORKLOADS: dict[str, dict] = {
                                         dtype=torch.bfloat16, seed=5),
     "decode_bf16_qwen25_05b": dict(kind="decode", batch=64, num_heads=14, kv_heads=2, head_dim=64,
                                    block_size=16, ctx=(512, 4096), dtype=torch.bfloat16, seed=6),
+    "prefill_bf16_qwen25_05b": dict(kind="prefill", num_seqs=8, num_heads=14, kv_heads=2,
+                                    head_dim=64, block_size=16, q_len=(256, 1024), prefix=0,
+                                    dtype=torch.bfloat16, seed=8),
+    "prefill_f32_h8_d64": dict(kind="prefill", num_seqs=4, num_heads=8, kv_heads=8, head_dim=64,
+                               block_size=16, q_len=(128, 512), prefix=0, dtype=torch.float32,
+                               seed=9),
 }
 
 

@@ -707,7 +707,7 @@ def test_prefill_dma_switch_rejects_bad_mode():
     (torch.float32, 8, 8, 64, 16, [1, 17, 40, 300], 32),   # eight rows per workgroup
     (torch.float32, 16, 4, 128, 16, [129, 5], 0),           # two rows x four heads
     (torch.float32, 16, 1, 32, 7, [50, 1], 14),             # n_rep 16: two head groups
-    (torch.bfloat16, 14, 2, 64, 16, [300, 77, 1], 64),      # Qwen2.5-0.5B attention shape
+    (torch.bfloat16, 14, 2, 64, 8, [300, 77, 1], 64),       # Qwen2.5-0.5B heads, 8-token pages
     (torch.float16, 8, 2, 64, 32, [90, 33], 32),
 ])
 def test_prefill_vector_kernel_shapes(device, dt, H, G, D, bs, lens, prefix):
