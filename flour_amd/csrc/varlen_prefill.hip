@@ -34,7 +34,7 @@
 //    The reference max may lag the running max by up to 8 (weights up to 2^8), so the output
 //    accumulator is rescaled only when some row's max grows past that. Fully masked tiles are
 //    skipped per wave; masks are evaluated only on tiles that cross the diagonal.
-//  * P.V precision: PV_F16 rounds P once to fp16 and widens bf16 V to fp16 (exact in range);
+//  * P.V precision: PV_F16 rounds P once to fp16 and converts bf16 V to fp16 (exact in range);
 //    PV_HILO splits P into hi + lo parts of the storage type (two MFMAs per product, ~16
 //    significant bits).
 #include <math.h>
@@ -90,27 +90,26 @@ __device__ __forceinline__ int swap_bits01(int x) {
 }
 
 // P.V arithmetic of the MFMA path.
-//  PV_F16:   P rounded once to fp16 (11 significant bits; P is in [0, 1]) and V widened
-//            exactly to fp16 when the pool is bf16 (exact for |v| < 65504, the fp16 range);
-//            one MFMA per product.
+//  PV_F16:   P rounded once to fp16 (11 significant bits; P is in [0, 2^8]) and V converted
+//            to fp16 when the pool is bf16 (exact in fp16's range, below); one MFMA per
+//            product.
 //  PV_HILO:  P split into hi + lo parts of the storage type (~16 significant bits), V in the
 //            storage type; two MFMAs per product.
 //  exact:    the fallback of PV_F16 for an item whose fp16 P.V cannot be trusted (below):
 //            V stays bf16, P is split into bf16 hi + lo parts, and the running max is kept
 //            exact (no slack), so every weight is at most 1 and |p v| stays in fp32 range.
 //
-// bf16 V in PV_F16 mode is widened to fp16 as v * 2^8, which fp16 holds exactly for every bf16
-// value with 2^-25 <= |v| <= 255 (0 stays 0); the output is scaled back by 2^-8. Outside that:
-//  * |v| >= 256, inf or NaN widen to inf or NaN and make the accumulator non-finite;
-//  * 0 < |v| < 2^-25 is rounded to the fp16 grid, an error of at most 2^-33 in v, hence at most
-//    2^-33 in any output (the weights sum to 1).
-// At the end of each item every wave checks its 32 x 128 output block: if it is not finite, or
-// if its largest |output| is below 2^-16 (where 2^-33 per element could reach 5e-4 of the
-// block's L2 norm), the workgroup recomputes the item in exact mode. Otherwise the block's error
-// from the widening is at most 5e-4 of its norm and that from rounding P to fp16 ~1.5e-4.
-static constexpr float PF_V_SCALE = 256.0f;          // 2^8
-static constexpr float PF_V_UNSCALE = 1.0f / 256.0f;
-static constexpr float PF_MIN_TRUSTED = 0x1p-16f;   // smallest block max the fp16 path keeps
+// bf16 V in PV_F16 mode is converted to fp16 (round to nearest even), which holds every bf16
+// value with 2^-17 <= |v| <= 65504 exactly, and 0. Outside that:
+//  * |v| >= 65520, inf or NaN become inf or NaN and make the accumulator non-finite;
+//  * 0 < |v| < 2^-17 is rounded to the fp16 grid (spacing 2^-24), an error of at most 2^-25 in
+//    v, hence at most 2^-25 in any output (the weights sum to 1).
+// At the end of each item every wave checks its output block (its valid rows x head_dim): if
+// it is not finite, or if its root mean square is below 2^-25 / 5e-4 (where the conversion's
+// error could exceed 5e-4 of the block's L2 norm), the workgroup recomputes the item in exact
+// mode. Otherwise the block's error from the conversion is at most 5e-4 of its norm and that
+// from rounding P to fp16 ~1.5e-4.
+static constexpr float PF_MIN_TRUSTED_RMS = 0x1p-25f / 5e-4f;  // ~6e-5
 enum { PV_F16 = 0, PV_HILO = 1 };
 
 static constexpr uint32_t PF_OOR = 0x80000000u;  // buffer offset past any pool: loads read 0
@@ -175,7 +174,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     constexpr int NMT = D / 32;        // 32-dim blocks of O^T = V^T P^T
     // V^T is staged as fp16 for PV_F16, as the storage type otherwise; K keeps the storage type.
     typedef typename std::conditional<PV == PV_F16, f16_t, T>::type TV;
-    // bf16 V is widened to fp16 scaled by 2^8 and each item's output blocks are checked at its
+    // bf16 V is converted to fp16 and each item's output blocks are checked at its
     // end (CHECK_V); a failed check recomputes the item in exact mode.
     constexpr bool CHECK_V = PV == PV_F16 && std::is_same<T, bf16_t>::value;
     // LDS tile buffers, each K then V:
@@ -748,13 +747,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     auto lds_store_v = [&](auto ex, int buf, u32x4* vd) {
         if (!v_on) return;  // head_dim 64: waves 4-7 stage no V
         if constexpr (CHECK_V && !decltype(ex)::value) {
-            // widen bf16 V to fp16 as v * 2^8 (exact for 2^-25 <= |v| <= 255 and 0)
+            // bf16 V to fp16 (exact for 2^-17 <= |v| <= 65504 and 0)
 #pragma unroll
             for (int j = 0; j < 2; j++)
 #pragma unroll
                 for (int x = 0; x < 4; x++)
-                    vd[j][x] = pack2<f16_t>(lo_f32<bf16_t>(vd[j][x]) * PF_V_SCALE,
-                                            hi_f32<bf16_t>(vd[j][x]) * PF_V_SCALE);
+                    vd[j][x] = pack2<f16_t>(lo_f32<bf16_t>(vd[j][x]), hi_f32<bf16_t>(vd[j][x]));
         }
         const int col = sigma16(2 * v_tp);  // the pair stays adjacent under sigma16
 #pragma unroll
@@ -826,7 +824,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             qb[kk] = *reinterpret_cast<const u32x4*>(qr + 8 * ((2 * kk + h2) ^ (ql32 % CPR)));
     };
 
-    float out_scale = 1.0f;  // 2^-8 after the fp16 path over bf16 V (CHECK_V), else 1
     // Running state: the reference max m may lag the true running max by up to
     // PF_RESCALE_SLACK (weights then reach 2^8), which skips most accumulator rescales.
     float m = -INFINITY, lsum = 0.0f;
@@ -843,8 +840,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     auto store_output = [&](int sbuf) __attribute__((always_inline)) {
         const float l = lsum + wave_shfl_xor(lsum, 32);
         if (wave_active) {
-            // 0: an item that attends nothing; out_scale undoes the widening scale of V
-            const float inv = l > 0.0f ? out_scale / l : 0.0f;
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;  // 0: an item that attends nothing
             if constexpr (sizeof(TO) == 4) {
                 const int orow = wr0 + ql32;
                 if (orow < ql) {
@@ -1163,21 +1159,25 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                            it.last_page + 1);
     };
     auto item_window = [&](int k) __attribute__((always_inline)) { return window_of(fetch(k)); };
-    // Item-end check of the fp16 path (CHECK_V): true if this wave's output block is not finite
-    // or its largest |output| is below PF_MIN_TRUSTED (both in the 2^8-scaled accumulator:
-    // |o| / l is 2^8 times the output).
+    // Item-end check of the fp16 path (CHECK_V): true if this wave's output block (its valid
+    // rows) is not finite or its root mean square is below PF_MIN_TRUSTED_RMS. Lane (h2, q)
+    // holds 16 NMT outputs of row q, all scaled by the row's 1 / l.
     auto block_untrusted = [&]() __attribute__((always_inline)) {
-        float mx = 0.0f;
+        float ss = 0.0f;
 #pragma unroll
         for (int x = 0; x < NMT; x++)
 #pragma unroll
-            for (int y = 0; y < 16; y += 2)
-                mx = vmax(vmax(mx, __builtin_fabsf(o[x][y])), __builtin_fabsf(o[x][y + 1]));
+            for (int y = 0; y < 16; y++) ss = fmaf(o[x][y], o[x][y], ss);
         const float l = lsum + wave_shfl_xor(lsum, 32);
-        const bool nonfinite = !(mx < INFINITY);  // NaN compares false
-        const bool big = mx >= PF_MIN_TRUSTED * PF_V_SCALE * l;
-        return wave_active && (__builtin_amdgcn_ballot_w64(nonfinite) != 0 ||
-                               __builtin_amdgcn_ballot_w64(big) == 0);
+        const bool row_ok = wr0 + ql32 < ql;
+        const bool nonfinite = !(ss < INFINITY);  // NaN compares false
+        // sum over the valid rows of the block of (outputs)^2
+        float blk = row_ok && l > 0.0f ? ss / (l * l) : 0.0f;
+#pragma unroll
+        for (int o2 = 1; o2 < 64; o2 <<= 1) blk += wave_shfl_xor(blk, o2);
+        const float n = (float)(__popcll(__builtin_amdgcn_ballot_w64(row_ok)) * 16 * NMT);
+        const bool small = !(blk >= n * PF_MIN_TRUSTED_RMS * PF_MIN_TRUSTED_RMS);
+        return wave_active && (__builtin_amdgcn_ballot_w64(nonfinite) != 0 || small);
     };
     Item ci = fetch(0);
     prologue(ci, item_window(0), false);
@@ -1344,7 +1344,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         run_tiles(std::false_type{}, state);
         bool redo = false;
         if constexpr (CHECK_V) {
-            out_scale = PF_V_UNSCALE;
             if (n_kt > 0) {  // flags written before the last step's barrier
                 const u32x2 f = *reinterpret_cast<const u32x2*>(&redo_flag[PF_WAVES * (k & 1)]);
                 redo = uni((int)(f[0] | f[1])) != 0;
@@ -1355,7 +1354,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 win_next = load_window(bt, 64, last_page + 1);
                 start_tiles(std::true_type{});
                 run_tiles(std::true_type{}, 0);
-                out_scale = 1.0f;
             }
         }
         // output staging (DMA): the buffer of the item's last tile (the next item's first tiles
@@ -1386,7 +1384,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 
 // Staging copy of V for the DMA kernel: every 16-token page of each sequence's kv range,
 // rounded up to whole 64-token tiles, as V^T in fp16 (128 dims x 16 tokens, token sigma16(k) at
-// position k; bf16 values times 2^8 by the same conversion as the register-staged path), tokens
+// position k; bf16 values converted as on the register-staged path), tokens
 // past kv_len zero. Page p of sequence s and kv head h is at ((s * P + p) * kv_heads + h) * 4 KB,
 // P = 4 * ceil(max_blocks * block_size / 64) pages per sequence (the block table's capacity in
 // whole tiles). One four-wave workgroup per 64-token tile, one wave per page; tiles past a
@@ -1431,8 +1429,7 @@ __global__ __launch_bounds__(256) void prefill_v_stage_kernel(
         for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int x = 0; x < 4; x++)
-                v[j][x] = pack2<f16_t>(lo_f32<bf16_t>(v[j][x]) * PF_V_SCALE,
-                                       hi_f32<bf16_t>(v[j][x]) * PF_V_SCALE);
+                v[j][x] = pack2<f16_t>(lo_f32<bf16_t>(v[j][x]), hi_f32<bf16_t>(v[j][x]));
     }
     uint16_t* t = tp[wv];
     const int pos = sigma16(4 * m);

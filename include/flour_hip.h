@@ -24,9 +24,10 @@
  *   - Element types are given by the flour_dtype codes below. Scores, softmax and accumulators
  *     are fp32 and outputs are rounded to nearest-even. The matrix products take bf16/f16
  *     inputs exactly, with one exception: prefill over bf16 pools runs P.V on fp16 matrix
- *     cores with V widened as v * 2^8 (exact for 2^-25 <= |v| <= 255) and P rounded to fp16;
- *     a work item whose output is not finite or is all below 2^-16 in magnitude is recomputed
- *     with bf16 V and P split into two bf16 parts. Decode splits P into two 16-bit parts.
+ *     cores with V converted to fp16 (exact for 2^-17 <= |v| <= 65504) and P rounded to fp16;
+ *     a work item whose output is not finite or whose output block has a root mean square
+ *     below 2^-25 / 5e-4 (~6e-5) is recomputed with bf16 V and P split into two bf16 parts.
+ *     Decode splits P into two 16-bit parts.
  */
 #ifndef FLOUR_HIP_H
 #define FLOUR_HIP_H

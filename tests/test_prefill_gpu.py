@@ -151,16 +151,17 @@ def _check_scaled_bf16(got_bits: np.ndarray, got32: np.ndarray, ref: np.ndarray,
 
 @pytest.mark.parametrize("case", ["mixed", "tiny", "small", "large", "huge"])
 def test_prefill_v_outside_fp16_range(device, case):
-    """bf16 V far from unit scale. The default P.V runs on fp16 MFMAs over V widened to fp16 as
-    v * 2^8, exact for 2^-25 <= |v| <= 255; an item whose output block is not finite (a wider
-    value overflowed) or whose outputs are all below 2^-16 is recomputed in exact bf16 mode.
-    The reference accumulates probs @ v.to_dtype(F32) for any finite bf16 (cpu.rs:103-104).
+    """bf16 V far from unit scale. The default P.V runs on fp16 MFMAs over V converted to
+    fp16, exact for 2^-17 <= |v| <= 65504; an item whose output block is not finite (a value
+    overflowed fp16) or whose root mean square is below 2^-25 / 5e-4 is recomputed in exact
+    bf16 mode. The reference accumulates probs @ v.to_dtype(F32) for any finite bf16
+    (cpu.rs:103-104).
       mixed: rows of +-1e5, one row of +-3e38 and rows of 1e-30 among N(0, 1) rows, in the
              cached prefix and in the new rows (one huge row per sequence, so every weighted
              sum stays in the fp32 range, as in the reference);
-      tiny:  every V value scaled by 1e-30 (all outputs below 2^-16: exact mode);
-      small: every V value scaled by 1e-4 (the fp16 path, values down to 2^-25 exact);
-      large: every V value scaled by 300 (most overflow the widened range: exact mode);
+      tiny:  every V value scaled by 1e-30 (exact mode);
+      small: every V value scaled by 1e-4 (outputs of ~1e-6: exact mode);
+      large: every V value scaled by 300 (within fp16: the fp16 path);
       huge:  every V value scaled by 1e30."""
     c = make_prefill(3, 8, 2, 128, 16, (1, 1), prefix=64, dtype=torch.bfloat16, seed=23,
                      device=device, q_lens=[300, 77, 129])
