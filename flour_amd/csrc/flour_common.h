@@ -174,6 +174,21 @@ __device__ __forceinline__ float wave_shfl_xor(float x, int mask) {
     return __shfl_xor(x, mask, 64);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave without the LDS crossbar: a scan within each
+// 16-lane row from DPP row shifts (lanes shifted in from outside the row read 0), then each row
+// adds the totals of the rows before it (lanes 15, 31, 47, read into scalars).
+__device__ __forceinline__ int wave_incl_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(x, 15);
+    const int r1 = __builtin_amdgcn_readlane(x, 31);
+    const int r2 = __builtin_amdgcn_readlane(x, 47);
+    const int row = (int)(__lane_id() >> 4);
+    return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
 // Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48) with the gfx950
 // row-swap instructions (plain VALU ops, no LDS crossbar): permlane16_swap pairs lane l with
 // l^16, permlane32_swap pairs l with l^32.
@@ -191,6 +206,21 @@ __device__ __forceinline__ float sum_across_rows(float x) {
     x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
     const uint32_t v = __float_as_uint(x);
     auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// Sum over all 64 lanes, in every lane: DPP row rotations by 8, 4, 2, 1 sum each 16-lane row,
+// then the rows are summed with the row swaps.
+__device__ __forceinline__ float wave_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false));
+    return sum_across_rows(x);
+}
+// x + x of lane l^32 with one row swap (VALU) instead of an LDS permute.
+__device__ __forceinline__ float sum_across_halves(float x) {
+    const uint32_t u = __float_as_uint(x);
+    auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 

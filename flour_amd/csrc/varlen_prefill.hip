@@ -222,10 +222,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // Register staging shapes items per (level, sequence) entry (FLEX): a sequence's last,
     // partial query tile takes 4 heads x 64 rows or 8 heads x 32 rows per item instead of
     // 2 heads x 128, and the one-head items of two consecutive tiles (odd GQA groups) share
-    // one item of 256 rows; two more decode tables.
+    // one item of 256 rows.
     constexpr bool FLEX = !DMA;
-    constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1 +
-                               (FLEX ? 2 * (PF_FLEX_ENTRIES + 1) : 0);
+    constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1;
     constexpr int QSTAGE_BYTES = DMA ? 0 : PF_WAVES * PF_QSTAGE_ELEMS * 2;
     constexpr int SCHED_BYTES = 4 * SCHED_INTS > QSTAGE_BYTES ? 4 * SCHED_INTS : QSTAGE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t sched_raw[SCHED_BYTES];
@@ -235,10 +234,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int* const sched_cum = sched_fill + (PF_MAX_LEVELS + 1);  // [L]: items before level L
     int* const sched_cu = sched_cum + (PF_MAX_LEVELS + 2);    // cu_seqlens
     int* const sched_kv = sched_cu + (PF_MAX_SEQS + 1);       // clamped kv lengths
-    // FLEX: [e] items before (level, sequence) entry e of the list, in part 1 (multi-head
-    // items) and part 2 (one-head items)
-    int* const sched_pc1 = sched_kv + PF_MAX_SEQS;
-    int* const sched_pc2 = sched_pc1 + (PF_FLEX_ENTRIES + 1);
     static_assert(!FLEX || 4 * SCHED_INTS <= QSTAGE_BYTES, "decode tables fit the Q staging");
     // query tiles of a sequence; one with kv_len < q_len still has its tiles, whose items
     // attend nothing and write zero rows (as the generic path and the oracle do)
@@ -254,12 +249,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             const int x = lane * per + i;
             if (x < n) local += get(suffix ? n - 1 - x : x);
         }
-        int incl = local;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
+        const int incl = wave_incl_sum(local);
         int run = incl - local;
         for (int i = 0; i < per; i++) {
             const int x = lane * per + i;
@@ -269,7 +259,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 run += v;
             }
         }
-        return __shfl(incl, 63, 64);  // total
+        return __builtin_amdgcn_readlane(incl, 63);  // total
     };
     // Heads per item of a tile with r rows (FLEX): 8 for at most 32 rows, 4 for at most 64, else
     // 2, but at most the GQA group rounded up to a power of two, and always 2 for groups of 1
@@ -297,22 +287,67 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
     int total_items = 0, total_base = 0, total1 = 0;  // items; (level, sequence) pairs; part 1
     bool flex_on = false;
+    // ---- this workgroup's items, decoded into LDS. An entry holds {seq, qt, kv head, first
+    // head in group | log2(heads per item) << 16, q0, q_len, kv_len, kv tiles}.
+    //  * persistent: the item list is longest-first in two parts: the multi-head items of every
+    //    level, then (odd n_rep) the one-head items of a single tile, which cost about 0.7 of a
+    //    two-head item. Within a part, items go level by level, sequences by decreasing tile
+    //    count, then heads; a one-head item of tiles qt - 1 and qt sits in part 1 after tile
+    //    qt's multi-head items. The k-th item of workgroup b is number kG + b on even k and
+    //    kG + G-1-b on odd k (a snake over the list balances the workgroups without shared
+    //    state);
+    //  * otherwise: one workgroup per (level, sequence, pair); items past a sequence's last
+    //    tile exit at once.
+    __shared__ __attribute__((aligned(16))) int sched_items[PF_MAX_WG_ITEMS][8];
+    __shared__ int sched_nitems;
+    const int half_rep = n_rep >> 1;
+    int wg_items = 0;
+    // the snake's share of workgroup wg in a list of n items
+    auto items_of_wg = [&](int n) {
+        const int rounds = n / G, rem = n - rounds * G;
+        return min(rounds + (((rounds & 1) ? G - 1 - wg : wg) < rem ? 1 : 0), PF_MAX_WG_ITEMS);
+    };
+    // item k of this workgroup: tile NQ-1-level of sequence seq, heads h0 .. of kv head kvh
+    auto put_item = [&](int k, int seq, int level, int kvh, int h0, int lg) __attribute__((always_inline)) {
+        // first q / out row of the sequence: q_rows[seq] when given (the sequences of a mixed
+        // step, whose rows sit among other sequences' rows), else its cu_seqlens start
+        const int c0 = persistent ? sched_cu[seq] : cu_seqlens[seq];
+        const int q0 = q_rows ? q_rows[seq] : c0;
+        const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - c0;
+        const int kvl = persistent ? sched_kv[seq] : min(kv_lens[seq], kv_cap);
+        const int qt = NQ - 1 - level;
+        const int row_last = min(qt * PF_QT + (256 >> lg), ql) - 1;  // the item's last row
+        const bool ok = qt * PF_QT < ql;  // always true for persistent items
+        int* e = sched_items[k];
+        e[0] = seq;
+        e[1] = qt;
+        e[2] = kvh;
+        e[3] = h0 | (lg << 16);
+        e[4] = q0;
+        e[5] = ql;
+        e[6] = kvl;
+        // causal kv tiles; none when kv_len < q_len (the rows are written as zeros)
+        e[7] = (ok && kvl >= ql) ? (kvl - ql + row_last + 1 + PF_KT - 1) / PF_KT : 0;
+        return ok;
+    };
     if (persistent) {
         for (int i = tid; i <= num_seqs; i += PF_THREADS) sched_cu[i] = cu_seqlens[i];
         for (int i = tid; i < num_seqs; i += PF_THREADS) sched_kv[i] = min(kv_lens[i], kv_cap);
-        for (int v = tid; v <= NQ; v += PF_THREADS) sched_fill[v] = 0;
-        __syncthreads();
-        for (int sq = tid; sq < num_seqs; sq += PF_THREADS) atomicAdd(&sched_fill[seq_tiles(sq)], 1);
         __syncthreads();
         if (w == 0) {
-            // more[v] = sequences with a tile count above v (a suffix sum of the histogram)
+            // Wave 0 alone, without barriers (a wave's LDS operations complete in order):
+            // histogram of tile counts, more[v] = sequences with a tile count above v (its
+            // suffix sum), a stable counting sort by decreasing tile count, and the level
+            // offsets.
+            for (int v = lane; v <= NQ; v += 64) sched_fill[v] = 0;
+            __builtin_amdgcn_wave_barrier();
+            for (int sq = lane; sq < num_seqs; sq += 64) atomicAdd(&sched_fill[seq_tiles(sq)], 1);
+            __builtin_amdgcn_wave_barrier();
             wave_scan(NQ + 1, [&](int v) { return sched_fill[v]; },
                       [&](int v, int x) { sched_more[v] = x; }, true);
-        }
-        __syncthreads();
-        for (int v = tid; v <= NQ; v += PF_THREADS) sched_fill[v] = 0;
-        __syncthreads();
-        if (w == 0) {
+            __builtin_amdgcn_wave_barrier();
+            for (int v = lane; v <= NQ; v += 64) sched_fill[v] = 0;
+            __builtin_amdgcn_wave_barrier();
             // stable counting sort (every workgroup must build the same order): 64 sequences
             // at a time, a lane's rank among equal tile counts comes from ballots over the
             // count's bits (counts are at most PF_MAX_LEVELS < 1024)
@@ -329,10 +364,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 const int fill = sched_fill[n];
                 if (n > 0) sched_order[sched_more[n] + fill + rank] = sq;
                 if (rank == 0) sched_fill[n] = fill + __popcll(same);
+                __builtin_amdgcn_wave_barrier();
             }
-        }
-        __syncthreads();
-        if (w == 0) {
             // level L (tile qt = NQ-1-L) holds the sequences with more than qt tiles:
             // sched_cum[L] = sequences on the levels before L
             const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
@@ -344,8 +377,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         total_items = npairs * total_base;
         flex_on = FLEX && total_base <= PF_FLEX_ENTRIES;
         if (flex_on) {
-            // exclusive prefix sums of the entries' item counts in list order (level by level,
-            // sequences in tile-count order): each thread walks a contiguous run of entries
+            // Each thread walks a contiguous run of entries (level by level, sequences in
+            // tile-count order) twice: once for its item counts, whose exclusive prefix sums
+            // over the workgroup give each entry's first item in part 1 and part 2, then to
+            // decode the items of its entries that the snake deals to this workgroup.
             const int per = (total_base + PF_THREADS - 1) / PF_THREADS;
             const int e0 = min(tid * per, total_base), e1 = min(e0 + per, total_base);
             int L = 0, hi = NQ - 1;  // level of entry e0: last L with sched_cum[L] <= e0
@@ -365,15 +400,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                     i = 0;
                 }
             }
-            int x1 = s1, x2 = s2;  // inclusive scan within the wave
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y1 = __shfl_up(x1, o, 64), y2 = __shfl_up(x2, o, 64);
-                if (lane >= o) {
-                    x1 += y1;
-                    x2 += y2;
-                }
-            }
+            const int x1 = wave_incl_sum(s1), x2 = wave_incl_sum(s2);  // inclusive, in the wave
             if (lane == 63) {  // wave totals (sched_fill is free once the order is built)
                 sched_fill[2 * w] = x1;
                 sched_fill[2 * w + 1] = x2;
@@ -389,97 +416,65 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 t1 += a1;
                 t2 += a2;
             }
+            total1 = __builtin_amdgcn_readfirstlane(t1);
+            total_items = total1 + __builtin_amdgcn_readfirstlane(t2);
+            wg_items = items_of_wg(total_items);
             int r1 = b1 + x1 - s1, r2 = b2 + x2 - s2;
             L = L0;
             for (int e = e0, i = i0; e < e1; e++) {
+                const int seq = sched_order[i], qt = NQ - 1 - L;
                 int c1, c2;
-                entry_items(sched_order[i], NQ - 1 - L, c1, c2);
-                sched_pc1[e] = r1;
-                sched_pc2[e] = r2;
+                entry_items(seq, qt, c1, c2);
+                // list items a .. a + c - 1 of each part; item idx of round rd = idx / G goes to
+                // workgroup idx % G on even rounds, G-1 - idx % G on odd ones
+#pragma unroll
+                for (int part = 0; part < 2; part++) {
+                    const int a = part ? total1 + r2 : r1, c = part ? c2 : c1;
+                    for (int rd = a / G; rd * G < a + c && rd < wg_items; rd++) {
+                        const int idx = rd * G + ((rd & 1) ? G - 1 - wg : wg);
+                        if (idx < a || idx >= a + c) continue;
+                        const int p = idx - a;
+                        int level = L, kvh, h0, lg = 1;
+                        if (part) {
+                            kvh = p;
+                            h0 = n_rep - 1;
+                        } else {
+                            lg = tile_lg(seq, qt, seq_tiles(seq));
+                            if (lg == 1 && p >= kv_heads * half_rep) {  // 1 head x 256 rows from qt - 1
+                                kvh = p - kv_heads * half_rep;
+                                h0 = n_rep - 1;
+                                lg = 0;
+                                level = L + 1;
+                            } else if (lg == 1) {
+                                kvh = p / half_rep;
+                                h0 = 2 * (p - kvh * half_rep);
+                            } else {
+                                const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
+                                kvh = p / g;
+                                h0 = (p - kvh * g) << lg;
+                            }
+                        }
+                        put_item(rd, seq, level, kvh, h0, lg);
+                    }
+                }
                 r1 += c1;
                 r2 += c2;
-                if (++i == sched_more[NQ - 1 - L]) {
+                if (++i == sched_more[qt]) {
                     L++;
                     i = 0;
                 }
             }
-            if (tid == 0) {
-                sched_pc1[total_base] = t1;
-                sched_pc2[total_base] = t2;
-            }
-            __syncthreads();
-            total1 = __builtin_amdgcn_readfirstlane(t1);
-            total_items = total1 + __builtin_amdgcn_readfirstlane(t2);
-        }
-    }
-
-    // ---- this workgroup's items, decoded into LDS (one thread per item). An entry holds
-    // {seq, qt, kv head, first head in group | log2(heads per item) << 16, q0, q_len, kv_len,
-    // kv tiles}.
-    //  * persistent: the item list is longest-first in two parts: the multi-head items of every
-    //    level, then (odd n_rep) the one-head items of a single tile, which cost about 0.7 of a
-    //    two-head item. Within a part, items go level by level, sequences by decreasing tile
-    //    count, then heads; a one-head item of tiles qt - 1 and qt sits in part 1 after tile
-    //    qt's multi-head items. The k-th item of workgroup b is number kG + b on even k and kG + G-1-b on odd k
-    //    (a snake over the list balances the workgroups without shared state);
-    //  * otherwise: one workgroup per (level, sequence, pair); items past a sequence's last
-    //    tile exit at once.
-    __shared__ __attribute__((aligned(16))) int sched_items[PF_MAX_WG_ITEMS][8];
-    __shared__ int sched_nitems;
-    {
-        const int half_rep = n_rep >> 1;
-        const int np_full = kv_heads * half_rep, np_lone = kv_heads * (n_rep & 1);
-        int n_items = 0;
-        if (persistent) {
-            const int rounds = total_items / G, rem = total_items - rounds * G;
-            n_items = rounds + (((rounds & 1) ? G - 1 - wg : wg) < rem ? 1 : 0);
-            n_items = min(n_items, PF_MAX_WG_ITEMS);
         } else {
-            n_items = 1;
+            wg_items = items_of_wg(total_items);
         }
-        for (int k = tid; k < n_items; k += PF_THREADS) {
-            int seq, level, kvh, h0, lg = 1;  // h0: the item's first head in its GQA group
-            if (flex_on) {
-                // part 1: multi-head items, part 2: one-head items, each in list order; the
-                // entry of item idx is the last one whose prefix is <= its index in the part
-                const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
-                const bool part2 = idx >= total1;
-                const int ii = part2 ? idx - total1 : idx;
-                const int* pc = part2 ? sched_pc2 : sched_pc1;
-                int e = 0, he = total_base - 1;
-                while (e < he) {
-                    const int mid = (e + he + 1) >> 1;
-                    if (pc[mid] <= ii) e = mid; else he = mid - 1;
-                }
-                int lo = 0, hi = NQ - 1;  // last level L with sched_cum[L] <= e
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (sched_cum[mid] <= e) lo = mid; else hi = mid - 1;
-                }
-                level = lo;
-                seq = sched_order[e - sched_cum[lo]];
-                const int qt = NQ - 1 - lo;
-                const int p = ii - pc[e];
-                if (part2) {
-                    kvh = p;
-                    h0 = n_rep - 1;
-                } else {
-                    lg = tile_lg(seq, qt, seq_tiles(seq));
-                    if (lg == 1 && p >= kv_heads * half_rep) {  // 1 head x 256 rows from qt - 1
-                        kvh = p - kv_heads * half_rep;
-                        h0 = n_rep - 1;
-                        lg = 0;
-                        level = lo + 1;
-                    } else if (lg == 1) {
-                        kvh = p / half_rep;
-                        h0 = 2 * (p - kvh * half_rep);
-                    } else {
-                        const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
-                        kvh = p / g;
-                        h0 = (p - kvh * g) << lg;
-                    }
-                }
-            } else if (persistent) {
+    } else {
+        wg_items = 1;
+    }
+    if (!flex_on) {
+        const int np_full = kv_heads * half_rep, np_lone = kv_heads * (n_rep & 1);
+        for (int k = tid; k < wg_items; k += PF_THREADS) {
+            int seq, level, kvh, h0;  // h0: the item's first head in its GQA group
+            if (persistent) {
                 const int idx = k * G + ((k & 1) ? G - 1 - wg : wg);
                 const int n_full = np_full * total_base;
                 const bool lone = idx >= n_full;
@@ -505,30 +500,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                 kvh = hp / pairs_per_kv;
                 h0 = 2 * (hp - kvh * pairs_per_kv);
             }
-            // first q / out row of the sequence: q_rows[seq] when given (the sequences of a
-            // mixed step, whose rows sit among other sequences' rows), else its cu_seqlens start
-            const int c0 = persistent ? sched_cu[seq] : cu_seqlens[seq];
-            const int q0 = q_rows ? q_rows[seq] : c0;
-            const int ql = (persistent ? sched_cu[seq + 1] : cu_seqlens[seq + 1]) - c0;
-            const int kvl = persistent ? sched_kv[seq] : min(kv_lens[seq], kv_cap);
-            const int qt = NQ - 1 - level;
-            const int row_last = min(qt * PF_QT + (256 >> lg), ql) - 1;  // the item's last row
-            const bool ok = qt * PF_QT < ql;  // always true for persistent items
-            int* e = sched_items[k];
-            e[0] = seq;
-            e[1] = qt;
-            e[2] = kvh;
-            e[3] = h0 | (lg << 16);
-            e[4] = q0;
-            e[5] = ql;
-            e[6] = kvl;
-            // causal kv tiles; none when kv_len < q_len (the rows are written as zeros)
-            e[7] = (ok && kvl >= ql) ? (kvl - ql + row_last + 1 + PF_KT - 1) / PF_KT : 0;
+            const bool ok = put_item(k, seq, level, kvh, h0, 1);
             if (!persistent) sched_nitems = ok ? 1 : 0;
         }
-        if (persistent && tid == 0) sched_nitems = n_items;
-        __syncthreads();
     }
+    if (persistent && tid == 0) sched_nitems = wg_items;
+    __syncthreads();
     const int n_items = __builtin_amdgcn_readfirstlane(sched_nitems);
 
     // A work item (all fields workgroup-uniform); valid == 0 past the end of the list.
@@ -838,7 +815,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
     // ---- epilogue: lane (h2, q) holds dims 32 mt2 + 8 i + 4 h2 + j of query row wr0 + q
     auto store_output = [&](int sbuf) __attribute__((always_inline)) {
-        const float l = lsum + wave_shfl_xor(lsum, 32);
+        const float l = sum_across_halves(lsum);
         if (wave_active) {
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;  // 0: an item that attends nothing
             if constexpr (sizeof(TO) == 4) {
@@ -1168,13 +1145,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         for (int x = 0; x < NMT; x++)
 #pragma unroll
             for (int y = 0; y < 16; y++) ss = fmaf(o[x][y], o[x][y], ss);
-        const float l = lsum + wave_shfl_xor(lsum, 32);
+        const float l = sum_across_halves(lsum);
         const bool row_ok = wr0 + ql32 < ql;
         const bool nonfinite = !(ss < INFINITY);  // NaN compares false
         // sum over the valid rows of the block of (outputs)^2
         float blk = row_ok && l > 0.0f ? ss / (l * l) : 0.0f;
-#pragma unroll
-        for (int o2 = 1; o2 < 64; o2 <<= 1) blk += wave_shfl_xor(blk, o2);
+        blk = wave_sum(blk);
         const float n = (float)(__popcll(__builtin_amdgcn_ballot_w64(row_ok)) * 16 * NMT);
         const bool small = !(blk >= n * PF_MIN_TRUSTED_RMS * PF_MIN_TRUSTED_RMS);
         return wave_active && (__builtin_amdgcn_ballot_w64(nonfinite) != 0 || small);
