@@ -95,6 +95,29 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Sum / maximum over the lanes that hold the same slice of a row (lanes li + LPR g, every
+// lane receives the result): DPP rotations inside 16-lane rows by multiples of LPR, then the
+// row swaps for lanes l ^ 16 and l ^ 32. No LDS crossbar.
+template <int LPR, bool MAX>
+__device__ __forceinline__ float across_groups(float x) {
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    if constexpr (LPR <= 8) x = op(x, dpp_move<0x128>(x));  // row_ror:8
+    if constexpr (LPR <= 4) x = op(x, dpp_move<0x124>(x));  // row_ror:4
+    if constexpr (LPR <= 2) x = op(x, dpp_move<0x122>(x));  // row_ror:2
+    if constexpr (LPR <= 1) x = op(x, dpp_move<0x121>(x));  // row_ror:1
+    if constexpr (LPR <= 16) {
+        const uint32_t u = __float_as_uint(x);
+        auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    }
+    if constexpr (LPR <= 32) {
+        const uint32_t u = __float_as_uint(x);
+        auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    }
+    return x;
+}
+
 __device__ __forceinline__ void store_out(void* out, int out_dtype, int64_t idx, float v) {
     if (out_dtype == FLOUR_DTYPE_F32)
         static_cast<float*>(out)[idx] = v;
@@ -137,20 +160,15 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
             for (int s0 = 0; s0 < num_seqs && seq < 0; s0 += 64) {
                 const int sq = s0 + lane;
                 const int n = sq < num_seqs ? (cu_seqlens_q[sq + 1] - cu_seqlens_q[sq] + rows - 1) / rows : 0;
-                int incl = n;
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const int y = __shfl_up(incl, o, 64);
-                    if (lane >= o) incl += y;
-                }
+                const int incl = wave_incl_sum(n);
                 const int excl = base + incl - n;
                 const uint64_t hit = __ballot(n > 0 && x >= excl && x < excl + n);
                 if (hit) {
                     const int src = __ffsll((unsigned long long)hit) - 1;
                     seq = s0 + src;
-                    first = __shfl(x - excl, src, 64);
+                    first = __builtin_amdgcn_readlane(x - excl, src);
                 }
-                base += __shfl(incl, 63, 64);
+                base += __builtin_amdgcn_readlane(incl, 63);
             }
             if (lane == 0) {
                 found[0] = seq;
@@ -288,16 +306,13 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
 #pragma unroll
     for (int qi = 0; qi < NQ; qi++) {
         if (qi >= nq) break;
-        float M = m[qi];
-        for (int o = LPR; o < 64; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float M = across_groups<LPR, true>(m[qi]);
         const float f = (M == -INFINITY) ? 0.0f : exp2f(m[qi] - M);
-        float L = l[qi] * f;
-        for (int o = LPR; o < 64; o <<= 1) L += __shfl_xor(L, o, 64);
+        const float L = across_groups<LPR, false>(l[qi] * f);
         float* r = red + ((int64_t)w * NQ + qi) * stride;
 #pragma unroll
         for (int e = 0; e < VEC; e++) {
-            float a = acc[qi][e] * f;
-            for (int o = LPR; o < 64; o <<= 1) a += __shfl_xor(a, o, 64);
+            const float a = across_groups<LPR, false>(acc[qi][e] * f);
             if (grp == 0) r[2 + li * VEC + e] = a;
         }
         if (lane == 0) {

@@ -217,6 +217,14 @@ __device__ __forceinline__ float wave_sum(float x) {
     x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false));
     return sum_across_rows(x);
 }
+// Maximum over all 64 lanes (fmaxf: a NaN lane is ignored), in every lane, the same way.
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xf, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false)));
+    return max_across_rows(x);
+}
 // x + x of lane l^32 with one row swap (VALU) instead of an LDS permute.
 __device__ __forceinline__ float sum_across_halves(float x) {
     const uint32_t u = __float_as_uint(x);

@@ -163,12 +163,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
             const int b = lane * per + i;
             if (b < batch) local += decode_chunks(context_lens[b], max_ctx);
         }
-        int incl = local;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
+        const int incl = wave_incl_sum(local);
         int run = incl - local;
         for (int i = 0; i < per; i++) {
             const int b = lane * per + i;
@@ -598,19 +593,16 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
             mx = ws.ml[2 * ((int64_t)slot * n_rep + hh)];
             lx = ws.ml[2 * ((int64_t)slot * n_rep + hh) + 1];
         }
-        float bm = mx;
-        for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
-        const float m_new = fmaxf(M, bm);
+        const float m_new = fmaxf(M, wave_max(mx));
         const float w = (slot >= 0) ? fast_exp2(mx - m_new) : 0.0f;
-        float bl = w * lx;
-        for (int off = 32; off > 0; off >>= 1) bl += __shfl_xor(bl, off, 64);
+        const float bl = wave_sum(w * lx);
         const float c_old = (M == -INFINITY) ? 0.0f : fast_exp2(M - m_new);
         L = L * c_old + bl;
 #pragma unroll
         for (int i = 0; i < E; i++) O[i] *= c_old;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float wj = __shfl(w, j, 64);
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
             if (s0[j] >= 0) add(wj, v0[j]);
         }
         // The rest in groups of 8 unconditional loads (a missing piece reads the first piece's
@@ -622,12 +614,12 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(
             int sl[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                sl[j] = __shfl(slot, q + j, 64);
+                sl[j] = __builtin_amdgcn_readlane(slot, q + j);
                 v[j] = row(sl[j] >= 0 ? sl[j] : fslot);
             }
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float wj = __shfl(w, q + j, 64);
+                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), q + j));
                 if (sl[j] >= 0) add(wj, v[j]);
             }
         }
