@@ -220,18 +220,20 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
     }
 
     // ---- chunks of waves * RPL * SIMT_UNROLL rows: row j = c0 + (u * waves + w) * RPL + grp.
-    // The next chunk's rows are loaded while this one is computed.
+    // The next chunk's rows are loaded while this one is computed, and the block ids of the
+    // chunk after it are fetched with those loads, so a chunk's K/V loads never wait for a
+    // block-table read of their own. A block id is read whether or not its row is < kv_end
+    // (the index is clamped into the table row), so that it does not wait for the kv length:
+    // the first two chunks' K/V loads depend on one memory round trip (their block ids), not two.
     const int chunk = waves * RPL * SIMT_UNROLL;
-    // The block id of row j is read whether or not j < kv_end (the index is clamped into the
-    // table row), so that it does not wait for the kv length: a step's K/V loads then depend on
-    // one memory round trip (its block ids), not two.
-    auto load = [&](int c0, u32x4* kr, u32x4* vr, int* jr) __attribute__((always_inline)) {
-        int64_t ids[SIMT_UNROLL];
+    auto load_ids = [&](int c0, int* ids) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < SIMT_UNROLL; u++) {
             const int j = c0 + (u * waves + w) * RPL + grp;
             ids[u] = bt[min(j / block_size, max_blocks - 1)];
         }
+    };
+    auto load = [&](int c0, const int* ids, u32x4* kr, u32x4* vr, int* jr) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < SIMT_UNROLL; u++) {
             const int j = c0 + (u * waves + w) * RPL + grp;
@@ -240,7 +242,7 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
             if (j < kv_end) {
                 const int lb = j / block_size;
                 // clamped: a bad block id never leaves the pool
-                const int64_t phys = ids[u] < 0 ? 0 : (ids[u] > max_phys ? max_phys : ids[u]);
+                const int64_t phys = ids[u] < 0 ? 0 : (ids[u] > max_phys ? max_phys : (int64_t)ids[u]);
                 row = (phys * block_size + (j - lb * block_size)) * head_dim;
             }
             kr[u] = *reinterpret_cast<const u32x4*>(kbase + row);
@@ -291,13 +293,23 @@ __global__ __launch_bounds__(simt_max_waves(NQ) * 64) void attn_simt_kernel(
             }
         }
     };
-    load(0, ka, va, ja);  // unconditional, so that it need not wait for the kv length
+    // ids_a: block ids of the chunk that set A loads next, ids_b those of set B
+    int ids_a[SIMT_UNROLL], ids_b[SIMT_UNROLL];
+    load_ids(0, ids_a);  // unconditional, so that they need not wait for the kv length
+    load_ids(chunk, ids_b);
+    load(0, ids_a, ka, va, ja);
     for (int c0 = 0; c0 < kv_end; c0 += 2 * chunk) {
         const bool more = c0 + chunk < kv_end;
-        if (more) load(c0 + chunk, kb, vb, jb);
+        if (more) {
+            load(c0 + chunk, ids_b, kb, vb, jb);
+            if (c0 + 2 * chunk < kv_end) load_ids(c0 + 2 * chunk, ids_a);
+        }
         compute(ka, va, ja);
         if (!more) break;
-        if (c0 + 2 * chunk < kv_end) load(c0 + 2 * chunk, ka, va, ja);
+        if (c0 + 2 * chunk < kv_end) {
+            load(c0 + 2 * chunk, ids_a, ka, va, ja);
+            if (c0 + 3 * chunk < kv_end) load_ids(c0 + 3 * chunk, ids_b);
+        }
         compute(kb, vb, jb);
     }
 
