@@ -723,19 +723,20 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // `ex` true: exact mode, V is stored as bf16 without widening
     auto lds_store_v = [&](auto ex, int buf, u32x4* vd) {
         if (!v_on) return;  // head_dim 64: waves 4-7 stage no V
-        if constexpr (CHECK_V && !decltype(ex)::value) {
-            // bf16 V to fp16 (exact for 2^-17 <= |v| <= 65504 and 0)
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int x = 0; x < 4; x++)
-                    vd[j][x] = pack2<f16_t>(lo_f32<bf16_t>(vd[j][x]), hi_f32<bf16_t>(vd[j][x]));
-        }
         const int col = sigma16(2 * v_tp);  // the pair stays adjacent under sigma16
+        // V^T row 8 v_dg + e holds dim 8 v_dg + e of the thread's two tokens as one dword
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int wd = e >> 1;
-            const uint32_t pr = (e & 1) ? perm_hi16(vd[0][wd], vd[1][wd]) : perm_lo16(vd[0][wd], vd[1][wd]);
+            uint32_t pr;
+            if constexpr (CHECK_V && !decltype(ex)::value) {
+                // bf16 V to fp16 (exact for 2^-17 <= |v| <= 65504 and 0), packed straight into
+                // the token pair of one dim: no permute after the conversion
+                pr = (e & 1) ? pack2<f16_t>(hi_f32<bf16_t>(vd[0][wd]), hi_f32<bf16_t>(vd[1][wd]))
+                             : pack2<f16_t>(lo_f32<bf16_t>(vd[0][wd]), lo_f32<bf16_t>(vd[1][wd]));
+            } else {
+                pr = (e & 1) ? perm_hi16(vd[0][wd], vd[1][wd]) : perm_lo16(vd[0][wd], vd[1][wd]);
+            }
             *reinterpret_cast<uint32_t*>(&vb_ptr(buf)[(8 * v_dg + e) * PF_VPITCH + col]) = pr;
         }
     };
