@@ -536,10 +536,15 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     };
 
     // a wave's head in the item's group and its 32-row block: heads of 8 / hpi waves each
-    // (hpi = 1 << lg heads per item), so waves w and w + 4, which share a SIMD, take the same
-    // rows of two heads
+    // (hpi = 1 << lg heads per item). Waves w and w + 4 share a SIMD; the second four take their
+    // row blocks in mirrored order, so that each SIMD holds one early and one late block: on an
+    // item's last kv tiles, which only its later rows see, every SIMD then keeps one wave busy
+    // instead of half the SIMDs two.
     auto wave_hl = [&](const Item& it) { return it.h0 + ((w << it.lg) >> 3); };
-    auto wave_rb = [&](const Item& it) { return w & ((8 >> it.lg) - 1); };
+    auto wave_rb = [&](const Item& it) {
+        const int nb = 8 >> it.lg;  // row blocks per head
+        return w < 4 ? (w & (nb - 1)) : (nb - 1) - ((w - 4) & (nb - 1));
+    };
     const int max_phys = (int)(num_slots / block_size - 1);
     const uint32_t head_bytes = (uint32_t)(num_slots * D * (int64_t)sizeof(T));
 
