@@ -84,6 +84,12 @@ static constexpr int PF_MAX_LEVELS = 512;  // query tiles per sequence (65536 ro
 static constexpr int PF_MAX_WG_ITEMS = 256;  // items per workgroup
 // (level, sequence) entries up to which register staging shapes its items per entry
 static constexpr int PF_FLEX_ENTRIES = 4096;
+// Workgroups up to which register staging deals its last round by load (the load table lives
+// in LDS); a larger grid keeps the plain snake.
+static constexpr int PF_MAX_GRID = 256;
+// Item cost in the load-ranked deal, 5 per kv tile + 7: per-workgroup cycle counts of the
+// Llama-3-8B varlen batch fit about 3,950 cycles per kv tile and 5,560 per item.
+static constexpr int PF_COST_TILE = 5, PF_COST_ITEM = 7;
 
 __device__ __forceinline__ int swap_bits01(int x) {
     return (x & ~3) | ((x & 1) << 1) | ((x >> 1) & 1);
@@ -224,7 +230,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     // 2 heads x 128, and the one-head items of two consecutive tiles (odd GQA groups) share
     // one item of 256 rows.
     constexpr bool FLEX = !DMA;
-    constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1;
+    constexpr int LOAD_INTS = FLEX ? 3 * PF_MAX_GRID + 2 : 0;
+    constexpr int SCHED_INTS = 3 * PF_MAX_SEQS + 1 + 3 * (PF_MAX_LEVELS + 1) + 1 + LOAD_INTS;
     constexpr int QSTAGE_BYTES = DMA ? 0 : PF_WAVES * PF_QSTAGE_ELEMS * 2;
     constexpr int SCHED_BYTES = 4 * SCHED_INTS > QSTAGE_BYTES ? 4 * SCHED_INTS : QSTAGE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t sched_raw[SCHED_BYTES];
@@ -234,6 +241,13 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int* const sched_cum = sched_fill + (PF_MAX_LEVELS + 1);  // [L]: items before level L
     int* const sched_cu = sched_cum + (PF_MAX_LEVELS + 2);    // cu_seqlens
     int* const sched_kv = sched_cu + (PF_MAX_SEQS + 1);       // clamped kv lengths
+    // FLEX: [G + 1] differences of the per-workgroup loads of the deal, then (8-byte aligned)
+    // [PF_MAX_GRID] the items of the deal's last round, {seq | level << 11 | part << 20, index}
+    int* const sched_load = sched_kv + PF_MAX_SEQS;
+    constexpr int LAST_OFF = (4 * (SCHED_INTS - LOAD_INTS + PF_MAX_GRID + 1) + 7) & ~7;  // bytes
+    static_assert(!FLEX || LAST_OFF + 8 * PF_MAX_GRID <= 4 * SCHED_INTS, "deal tables fit");
+    static_assert(PF_MAX_SEQS <= 2048 && PF_MAX_LEVELS <= 512, "last-round entries pack in 21 bits");
+    int2* const sched_last = reinterpret_cast<int2*>(sched_raw + LAST_OFF);
     static_assert(!FLEX || 4 * SCHED_INTS <= QSTAGE_BYTES, "decode tables fit the Q staging");
     // query tiles of a sequence; one with kv_len < q_len still has its tiles, whose items
     // attend nothing and write zero rows (as the generic path and the oracle do)
@@ -295,7 +309,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     //    count, then heads; a one-head item of tiles qt - 1 and qt sits in part 1 after tile
     //    qt's multi-head items. The k-th item of workgroup b is number kG + b on even k and
     //    kG + G-1-b on odd k (a snake over the list balances the workgroups without shared
-    //    state);
+    //    state), except that register staging deals the last round by the workgroups' load;
     //  * otherwise: one workgroup per (level, sequence, pair); items past a sequence's last
     //    tile exit at once.
     __shared__ __attribute__((aligned(16))) int sched_items[PF_MAX_WG_ITEMS][8];
@@ -333,6 +347,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     if (persistent) {
         for (int i = tid; i <= num_seqs; i += PF_THREADS) sched_cu[i] = cu_seqlens[i];
         for (int i = tid; i < num_seqs; i += PF_THREADS) sched_kv[i] = min(kv_lens[i], kv_cap);
+        if constexpr (FLEX)
+            for (int i = tid; i <= G && G <= PF_MAX_GRID; i += PF_THREADS) sched_load[i] = 0;
         __syncthreads();
         if (w == 0) {
             // Wave 0 alone, without barriers (a wave's LDS operations complete in order):
@@ -418,50 +434,127 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
             total1 = __builtin_amdgcn_readfirstlane(t1);
             total_items = total1 + __builtin_amdgcn_readfirstlane(t2);
-            wg_items = items_of_wg(total_items);
-            int r1 = b1 + x1 - s1, r2 = b2 + x2 - s2;
-            L = L0;
-            for (int e = e0, i = i0; e < e1; e++) {
-                const int seq = sched_order[i], qt = NQ - 1 - L;
-                int c1, c2;
-                entry_items(seq, qt, c1, c2);
-                // list items a .. a + c - 1 of each part; item idx of round rd = idx / G goes to
-                // workgroup idx % G on even rounds, G-1 - idx % G on odd ones
-#pragma unroll
-                for (int part = 0; part < 2; part++) {
-                    const int a = part ? total1 + r2 : r1, c = part ? c2 : c1;
-                    for (int rd = a / G; rd * G < a + c && rd < wg_items; rd++) {
-                        const int idx = rd * G + ((rd & 1) ? G - 1 - wg : wg);
-                        if (idx < a || idx >= a + c) continue;
-                        const int p = idx - a;
-                        int level = L, kvh, h0, lg = 1;
-                        if (part) {
-                            kvh = p;
-                            h0 = n_rep - 1;
-                        } else {
-                            lg = tile_lg(seq, qt, seq_tiles(seq));
-                            if (lg == 1 && p >= kv_heads * half_rep) {  // 1 head x 256 rows from qt - 1
-                                kvh = p - kv_heads * half_rep;
-                                h0 = n_rep - 1;
-                                lg = 0;
-                                level = L + 1;
-                            } else if (lg == 1) {
-                                kvh = p / half_rep;
-                                h0 = 2 * (p - kvh * half_rep);
-                            } else {
-                                const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
-                                kvh = p / g;
-                                h0 = (p - kvh * g) << lg;
-                            }
-                        }
-                        put_item(rd, seq, level, kvh, h0, lg);
+            // this run's first item of part 1 and of part 2, as list indices
+            const int a1_0 = b1 + x1 - s1, a2_0 = total1 + b2 + x2 - s2;
+            // walks this thread's entries: fn(seq, qt, L, first item and count of part 1, of part 2)
+            auto walk = [&](auto&& fn) {
+                int L = L0, a1 = a1_0, a2 = a2_0;
+                for (int e = e0, i = i0; e < e1; e++) {
+                    const int seq = sched_order[i], qt = NQ - 1 - L;
+                    int c1, c2;
+                    entry_items(seq, qt, c1, c2);
+                    fn(seq, qt, L, a1, c1, a2, c2);
+                    a1 += c1;
+                    a2 += c2;
+                    if (++i == sched_more[qt]) {  // levels are never empty once started
+                        L++;
+                        i = 0;
                     }
                 }
-                r1 += c1;
-                r2 += c2;
-                if (++i == sched_more[qt]) {
-                    L++;
-                    i = 0;
+            };
+            // item p of part `part` of entry (seq, tile qt on level L), into slot k
+            auto put_entry_item = [&](int k, int part, int p, int seq, int qt, int L) {
+                int level = L, kvh, h0, lg = 1;
+                if (part) {
+                    kvh = p;
+                    h0 = n_rep - 1;
+                } else {
+                    lg = tile_lg(seq, qt, seq_tiles(seq));
+                    if (lg == 1 && p >= kv_heads * half_rep) {  // 1 head x 256 rows from qt - 1
+                        kvh = p - kv_heads * half_rep;
+                        h0 = n_rep - 1;
+                        lg = 0;
+                        level = L + 1;
+                    } else if (lg == 1) {
+                        kvh = p / half_rep;
+                        h0 = 2 * (p - kvh * half_rep);
+                    } else {
+                        const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
+                        kvh = p / g;
+                        h0 = (p - kvh * g) << lg;
+                    }
+                }
+                put_item(k, seq, level, kvh, h0, lg);
+            };
+            // Rounds 0 .. R-2 follow the snake: item idx of round rd = idx / G goes to workgroup
+            // idx % G on even rounds, G-1 - idx % G on odd ones. From three rounds on, the last
+            // round is dealt by load instead: with every workgroup's cost over the earlier rounds
+            // (5 per kv tile + 7 per item), its items in list order go to the workgroups by
+            // increasing cost (ties by index), so the longest of them land where the snake left
+            // the least work (with two rounds the snake already pairs long with short). Every
+            // workgroup computes the same costs and so the same ranks.
+            const int rounds = (total_items + G - 1) / G;
+            const bool ranked = rounds >= 3 && rounds <= PF_MAX_WG_ITEMS && G <= PF_MAX_GRID;
+            const int cut = ranked ? (rounds - 1) * G : total_items;
+            wg_items = ranked ? rounds - 1 : items_of_wg(total_items);
+            walk([&](int seq, int qt, int L, int a1, int c1, int a2, int c2) {
+#pragma unroll
+                for (int part = 0; part < 2; part++) {
+                    const int a = part ? a2 : a1, c = part ? c2 : c1;
+                    for (int rd = a / G; rd * G < a + c && rd < wg_items; rd++) {
+                        const int idx = rd * G + ((rd & 1) ? G - 1 - wg : wg);
+                        if (idx >= a && idx < a + c) put_entry_item(rd, part, idx - a, seq, qt, L);
+                    }
+                }
+                if (!ranked) return;
+                // the entry's items of the last round, for the workgroup that ranks there
+#pragma unroll
+                for (int part = 0; part < 2; part++) {
+                    const int a = part ? a2 : a1, end = a + (part ? c2 : c1);
+                    for (int idx = max(a, cut); idx < end; idx++)
+                        sched_last[idx - cut] = int2{seq | (L << 11) | (part << 20), idx - a};
+                }
+                // the entry's items before the cut add their cost to the workgroups the snake
+                // gives them: per round one contiguous range of workgroups, as differences. All
+                // items of an entry share its kv tile count (a one-head item of tiles qt - 1 and
+                // qt ends on tile qt's last row).
+                const int ql = sched_cu[seq + 1] - sched_cu[seq], kvl = sched_kv[seq];
+                const int row_end = min((qt + 1) * PF_QT, ql);
+                const int n_kt = kvl >= ql ? (kvl - ql + row_end + PF_KT - 1) / PF_KT : 0;
+                const int cost = PF_COST_TILE * n_kt + PF_COST_ITEM;
+#pragma unroll
+                for (int part = 0; part < 2; part++) {
+                    const int a = part ? a2 : a1, end = min(a + (part ? c2 : c1), cut);
+                    for (int rd = a / G; rd * G < end; rd++) {
+                        const int p0 = max(a, rd * G) - rd * G, p1 = min(end, rd * G + G) - rd * G;
+                        atomicAdd(&sched_load[(rd & 1) ? G - p1 : p0], cost);
+                        atomicAdd(&sched_load[(rd & 1) ? G - p0 : p1], -cost);
+                    }
+                }
+            });
+            if (ranked) {
+                __syncthreads();
+                // Every wave ranks this workgroup by itself (no further barrier): lane l holds
+                // the loads of workgroups 4l .. 4l+3, inclusive prefix sums of the differences.
+                static_assert(PF_MAX_GRID <= 256, "four workgroups per lane");
+                int x[4], local = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    x[j] = 4 * lane + j < G ? sched_load[4 * lane + j] : 0;
+                    local += x[j];
+                }
+                int run = wave_incl_sum(local) - local;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    run += x[j];
+                    x[j] = run;
+                }
+                const int jm = wg & 3;
+                const int mine = __builtin_amdgcn_readlane(
+                    jm == 0 ? x[0] : jm == 1 ? x[1] : jm == 2 ? x[2] : x[3], wg >> 2);
+                int rank = 0;  // workgroups with less load, or as much and a lower index
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int b = 4 * lane + j;
+                    rank += __popcll(__ballot(b < G && (x[j] < mine || (x[j] == mine && b < wg))));
+                }
+                if (__builtin_amdgcn_readfirstlane(rank) < total_items - cut) {
+                    wg_items = rounds;
+                    if (tid == 0) {
+                        const int2 d = sched_last[rank];
+                        const int L = (d.x >> 11) & 511;
+                        put_entry_item(rounds - 1, d.x >> 20, d.y, d.x & 2047, NQ - 1 - L, L);
+                    }
                 }
             }
         } else {
