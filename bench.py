@@ -614,8 +614,17 @@ def bench_prefill(torch, ops, case, steps, warmup, theta=500000.0):
     a_ms = loop_timed(torch, each(attn_i), steps, 1)
     r_ms = loop_timed(torch, each(rope_i), steps, 1)
     del sets
+    # The KV write's practical ceiling at its size: one contiguous device copy of the same
+    # bytes (the new K and V rows), timed the same way over as many cold copies.
+    nb = case.k_new.nbytes + case.v_new.nbytes
+    srcs = [torch.empty(nb, dtype=torch.uint8, device=case.q.device) for _ in range(n)]
+    dsts = [torch.empty(nb, dtype=torch.uint8, device=case.q.device) for _ in range(n)]
+    c_ms = loop_timed(torch, rotating([(lambda i=i: dsts[i].copy_(srcs[i])) for i in range(n)]),
+                      steps, 1)
+    del srcs, dsts
     flops = case.flops()
     return dict(ms_per_step=wall_ms, attn_ms=a_ms, write_ms=w_ms, flops=flops, copies=n,
+                copy_ms=c_ms, copy_gbs=2 * nb / (c_ms * 1e-3) / 1e9,
                 tflops=flops / (a_ms * 1e-3) / 1e12, write_bytes=case.write_bytes(),
                 write_gbs=case.write_bytes() / (w_ms * 1e-3) / 1e9,
                 causal_pairs=case.causal_pairs(), rope_ms=r_ms, rope_bytes=rope_bytes(case),
@@ -644,7 +653,10 @@ def prefill_line(torch, ops, case, name, cfg, args):
                      "avg_launch_us": round(r["attn_ms"] * 1e3, 3), "traffic": read_traffic(name)},
         "kv_write": {"GB/s": round(r["write_gbs"], 1), "hbm_frac": round(r["write_gbs"] / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(r["write_ms"] * 1e3, 3), "bytes": r["write_bytes"],
-                     "traffic": read_traffic(name.replace("prefill_", "kv_write_"))},
+                     "traffic": read_traffic(name.replace("prefill_", "kv_write_")),
+                     "same_bytes_copy": {"GB/s": round(r["copy_gbs"], 1),
+                                         "hbm_frac": round(r["copy_gbs"] / HBM_PEAK_GBS, 4),
+                                         "avg_launch_us": round(r["copy_ms"] * 1e3, 3)}},
         "rope_kv_write": {"GB/s": round(r["rope_gbs"], 1), "hbm_frac": round(r["rope_gbs"] / HBM_PEAK_GBS, 4),
                           "avg_launch_us": round(r["rope_ms"] * 1e3, 3), "bytes": r["rope_bytes"]},
     }
@@ -800,6 +812,7 @@ def main():
                      "kv_write_traffic": read_traffic(nm.replace("prefill_", "kv_write_")),
                      "kv_write_GB/s": round(rr["write_gbs"], 1),
                      "kv_write_us": round(rr["write_ms"] * 1e3, 2),
+                     "same_bytes_copy_GB/s": round(rr["copy_gbs"], 1),
                      "rope_kv_write_GB/s": round(rr["rope_gbs"], 1),
                      "rope_kv_write_us": round(rr["rope_ms"] * 1e3, 2),
                      "step_ms": round(rr["ms_per_step"], 4)}
