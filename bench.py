@@ -257,8 +257,11 @@ def bench_batch_decode(torch, steps: int, warmup: int, cpu: bool, cpu_seconds: f
     head_dim 128, bf16, block 16): 64 sequences with the decode workload's seeded contexts
     U[512, 4096] live in one KvBatch pool. A step is one flour_kv_batch_step (one new row per
     sequence: allocation + plan upload) and, for each of the 32 layers, the KV write of the 64
-    new rows and paged decode attention over the whole batch. `kernels_ms` times the same 64
-    launches with no step call between them, so step_ms - kernels_ms is the host share."""
+    new rows and paged decode attention over the whole batch, as one
+    flour_kv_batch_write_kv_attention call (one decode launch that writes the new rows first,
+    plus its merge). `kernels_ms` times the same layers with no step call between them, so
+    step_ms - kernels_ms is the host share; `kernels_two_launch_ms` the same with the KV write
+    as its own launch."""
     import types
 
     from flour_amd.kv_cache import KvBatch
@@ -289,8 +292,7 @@ def bench_batch_decode(torch, steps: int, warmup: int, cpu: bool, cpu_seconds: f
 
     def layers():
         for layer in range(L):
-            b.write_kv(layer, k[layer], v[layer])
-            b.attention(layer, q[layer], scale, out=out[layer])
+            b.write_kv_attention(layer, k[layer], v[layer], q[layer], scale, out=out[layer])
 
     def step():
         b.step(sids, ones)
@@ -300,6 +302,12 @@ def bench_batch_decode(torch, steps: int, warmup: int, cpu: bool, cpu_seconds: f
     step_ms = loop_timed(torch, step, steps, warmup)
     t1 = sum(b.len(s) for s in sids)
     kern_ms = loop_timed(torch, layers, steps, warmup)
+    lib = __import__("flour_amd._lib", fromlist=["lib"]).lib()
+    lib.flour_hip_set_batch_fuse(0)
+    try:
+        kern2_ms = loop_timed(torch, layers, steps, warmup)
+    finally:
+        lib.flour_hip_set_batch_fuse(1)
     # mean live rows over the timed steps (each step adds one row per sequence)
     rows = t1 - B * (steps - 1) / 2.0
     nb = sum(len(b.blocks(s)) for s in sids)
@@ -307,7 +315,7 @@ def bench_batch_decode(torch, steps: int, warmup: int, cpu: bool, cpu_seconds: f
     nbytes = int(L * per_layer)
     assert t1 - t0 == B * (warmup + steps)
     r = {"sequences": B, "layers": L, "step_ms": round(step_ms, 4),
-         "kernels_ms": round(kern_ms, 4),
+         "kernels_ms": round(kern_ms, 4), "kernels_two_launch_ms": round(kern2_ms, 4),
          "host_share": round(max(0.0, step_ms - kern_ms) / step_ms, 4),
          "tokens/s": round(B / (step_ms * 1e-3), 1), "algorithmic_bytes": nbytes,
          "GB/s": round(nbytes / (step_ms * 1e-3) / 1e9, 1),

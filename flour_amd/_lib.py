@@ -113,6 +113,9 @@ SIGNATURES: dict[str, tuple] = {
                                               _vp, _c_i64, _c_i64, _vp, _vp, _c_int, _vp]),
     "flour_kv_batch_attention": (_c_int, [_vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _c_int,
                                           _c_i64, _c_i64, _c_f, _vp]),
+    "flour_kv_batch_write_kv_attention": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_i64, _vp,
+                                                   _c_int, _c_i64, _c_i64, _vp, _c_int, _c_i64,
+                                                   _c_i64, _c_f, _vp]),
     "flour_kv_batch_pool": (_c_int, [_vp, _c_int, _vp, _vp, _vp]),
     "flour_kv_cache_pool": (_c_int, [_vp, _c_int, _vp, _vp, _vp]),
 }
@@ -160,6 +163,7 @@ EXTRA_SIGNATURES: dict[str, tuple] = {
     "flour_hip_set_prefill_persistent": (_c_int, [_c_int]),
     "flour_hip_set_prefill_dma": (_c_int, [_c_int]),
     "flour_hip_set_batch_split": (_c_int, [_c_int]),
+    "flour_hip_set_batch_fuse": (_c_int, [_c_int]),
     "flour_hip_empty_launch": (_c_int, [_vp]),
 }
 

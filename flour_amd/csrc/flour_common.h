@@ -282,6 +282,22 @@ int paged_decode_rows(void* out, int out_dtype, const void* q, const void* k_poo
                       int kv_heads, int head_dim, int block_size, int64_t num_slots,
                       int max_context_len, float scale, int dtype, void* workspace,
                       size_t workspace_bytes, void* stream);
+// Decode step of a batch (one new row per sequence) with the step's KV write fused into the
+// decode launch (kv_batch.cpp): the new K / V row of entry b and kv head g, at k_new / v_new +
+// b * new_stride_tok + g * new_stride_head elements, goes to pool slot new_slots[b] (none outside
+// [0, num_slots)) and is attended as position context_lens[b] - 1. The result equals
+// flour_hip_kv_write followed by flour_hip_paged_decode when every new_slots[b] is the block
+// table's slot of position context_lens[b] - 1 and no other entry's blocks hold it.
+// FLOUR_ERR_UNSUPPORTED before any launch when the matrix-core decode does not take the shape,
+// the pages are not 16 tokens, or the new rows are not aligned to a lane's share of a row (16
+// bytes at head_dim 128, 8 at 64).
+int paged_decode_write_kv(void* out, int out_dtype, const void* q, void* k_pool, void* v_pool,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          const int32_t* context_lens, int batch, int num_heads, int kv_heads,
+                          int head_dim, int block_size, int64_t num_slots, int max_context_len,
+                          float scale, int dtype, void* workspace, size_t workspace_bytes,
+                          const void* k_new, const void* v_new, int64_t new_stride_tok,
+                          int64_t new_stride_head, const int32_t* new_slots, void* stream);
 int varlen_prefill_rows(void* out, int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,
                         const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                         const void* k_pool, const void* v_pool, const int32_t* cu_seqlens_q,

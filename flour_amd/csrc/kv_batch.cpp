@@ -36,6 +36,9 @@ namespace host {
 // 1: a mixed step's one-row sequences run on the decode kernel (default); 0: every row of a
 // mixed step on the prefill kernel. A tuning / test switch.
 static int g_batch_split = 1;
+// Decode steps through flour_kv_batch_write_kv_attention take the fused launch (1) or the KV
+// write and the attention as two launches (0); a tuning / test switch.
+static int g_batch_fuse = 1;
 
 struct KvBatchImpl {
     int num_layers, max_seqs, max_seq_len, max_tokens, num_heads, kv_heads, head_dim,
@@ -67,6 +70,9 @@ struct KvBatchImpl {
     // (pf_max_q rows at most, pf_total in all)
     bool plan_mixed = false;
     int plan_n_dec = 0, plan_dec_max_ctx = 0, plan_pf_max_q = 0, plan_pf_total = 0;
+    // decode step whose new positions all sit in blocks held by their sequence alone (reference
+    // count 1), so no other sequence of the step reads them: the fused KV write may run
+    bool plan_private = false;
 
     KvBatchImpl(int L, int nblk, int nseq, int max_len, int max_tok, int H, int G, int D, int bs,
                 int dt)
@@ -394,6 +400,11 @@ struct KvBatchImpl {
         plan_dec_max_ctx = dec_max_ctx;
         plan_pf_max_q = pf_max_q;
         plan_pf_total = (int)(total - n_dec);
+        plan_private = decode;
+        for (int i = 0; i < n && plan_private; i++) {
+            const BlockTable& t = tables[ids[i]];
+            plan_private = allocator.ref_count(t.blocks()[(t.len() - 1) / block_size]) == 1;
+        }
         return FLOUR_OK;
     }
     // allocate_kv(ids[i], q[i]) for every sequence of the step, then plan(): all checks
@@ -682,6 +693,38 @@ extern "C" int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void
                                        x.num_slots, scale, x.dtype, x.d_pf_ws, x.pf_ws_bytes,
                                        stream);
 }
+extern "C" int flour_kv_batch_write_kv_attention(flour_kv_batch* b, int layer, const void* k,
+                                                 const void* v, int64_t kv_stride_tok,
+                                                 int64_t kv_stride_head, const void* q,
+                                                 int num_heads, int64_t q_stride_tok,
+                                                 int64_t q_stride_head, void* out, int out_dtype,
+                                                 int64_t o_stride_tok, int64_t o_stride_head,
+                                                 float scale, void* stream) {
+    clear_error();
+    BATCH_NEED(b, "kv_batch: null");
+    KvBatchImpl& x = b->b;
+    if (int rc = x.need_plan(layer)) return rc;
+    BATCH_NEED(num_heads > 0 && num_heads <= x.num_heads && num_heads % x.kv_heads == 0,
+               "kv_batch: %d query heads (built for up to %d, %d kv heads)", num_heads,
+               x.num_heads, x.kv_heads);
+    const bool packed = q_stride_head == x.head_dim &&
+                        q_stride_tok == (int64_t)num_heads * x.head_dim &&
+                        o_stride_head == x.head_dim &&
+                        o_stride_tok == (int64_t)num_heads * x.head_dim;
+    if (x.plan_decode && x.plan_private && g_batch_fuse && packed) {
+        const int rc = paged_decode_write_kv(
+            out, out_dtype, q, x.k_pools[layer], x.v_pools[layer], x.d_tables(), x.max_blocks,
+            x.d_lens(), x.plan_n, num_heads, x.kv_heads, x.head_dim, x.block_size, x.num_slots,
+            x.plan_max_ctx, scale, x.dtype, x.d_ws, x.ws_bytes, k, v, kv_stride_tok,
+            kv_stride_head, x.d_slots(), stream);
+        if (rc != FLOUR_ERR_UNSUPPORTED) return rc;
+        clear_error();  // nothing launched: the two-launch form
+    }
+    if (int rc = flour_kv_batch_write_kv(b, layer, k, v, kv_stride_tok, kv_stride_head, stream))
+        return rc;
+    return flour_kv_batch_attention(b, layer, q, num_heads, q_stride_tok, q_stride_head, out,
+                                    out_dtype, o_stride_tok, o_stride_head, scale, stream);
+}
 extern "C" int flour_kv_batch_pool(const flour_kv_batch* b, int layer, void** k_pool,
                                    void** v_pool, int64_t* num_slots) {
     clear_error();
@@ -695,6 +738,10 @@ extern "C" int flour_kv_batch_pool(const flour_kv_batch* b, int layer, void** k_
     return FLOUR_OK;
 }
 
+extern "C" int flour_hip_set_batch_fuse(int on) {
+    flour::host::g_batch_fuse = on ? 1 : 0;
+    return FLOUR_OK;
+}
 extern "C" int flour_hip_set_batch_split(int on) {
     flour::host::g_batch_split = on ? 1 : 0;
     return FLOUR_OK;

@@ -94,6 +94,14 @@ struct DecodeWs {
     // continuous-batching step runs its one-row sequences, scattered among the packed rows of
     // longer ones, as one decode batch)
     const int32_t* rows;
+    // Decode step of a batch with its KV write fused in (the kernel's FUSE instantiation): the
+    // new K / V row of entry b and kv head g at k_new / v_new + b * new_st + g * new_sh
+    // (elements), written to pool slot new_slots[b] (skipped outside [0, num_slots)) before the
+    // attention reads it.
+    const void* k_new;
+    const void* v_new;
+    int64_t new_st, new_sh;
+    const int32_t* new_slots;
 };
 
 static int g_wg_override = 0;  // tuning / test hook: number of waves (0 = one resident round)
@@ -140,7 +148,7 @@ __device__ __forceinline__ int64_t owner_wg(int64_t x, int64_t total, int64_t n)
 // One wave per workgroup; each wave owns one contiguous range of the chunk list. D is the head
 // dim, 128 or 64. A lane's K/V share of a 16-token tile is rows 4lg .. 4lg + 3 at 16-byte
 // (D 128: dims 8lc ..) or 8-byte (D 64: dims 4lc ..) width, so a wave reads whole rows.
-template <typename T, typename TO, bool BS16, int D>
+template <typename T, typename TO, bool BS16, int D, bool FUSE>
 __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     TO* __restrict__ out, const T* __restrict__ q, const T* __restrict__ k_pool,
     const T* __restrict__ v_pool, const int32_t* __restrict__ block_tables, int max_blocks,
@@ -374,10 +382,15 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // (r < 4, nn < NV): D / 4 contiguous dims.
     auto epilogue = [&](int b, int g, bool complete, bool first_piece) {
         lsum = sum_across_rows(lsum);
+        // FUSE: lg made opaque here, so the per-lane output addresses are formed at the store
+        // instead of being hoisted out of the stream as 64-bit values (which spill in that
+        // instantiation, and a spill reload waits for every chunk load in flight)
+        int lgo = lg;
+        if constexpr (FUSE) asm volatile("" : "+v"(lgo));
         if (lc < n_rep) {
             if (complete) {  // whole pair in this range: final output
                 const int64_t row = ws.rows ? (int64_t)ws.rows[b] : (int64_t)b;
-                TO* o = out + (row * num_heads + (int64_t)g * n_rep + lc) * D + (D / 4) * lg;
+                TO* o = out + (row * num_heads + (int64_t)g * n_rep + lc) * D + (D / 4) * lgo;
                 const float inv = 1.0f / lsum;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
@@ -400,7 +413,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
                 }
             } else {  // partial row for the merge kernel
                 const int64_t pidx = (2 * wgi + (first_piece ? 0 : 1)) * n_rep + lc;
-                float* o = ws.o + pidx * D + (D / 4) * lg;
+                float* o = ws.o + pidx * D + (D / 4) * lgo;
 #pragma unroll
                 for (int r = 0; r < 4; r++)
 #pragma unroll
@@ -424,7 +437,82 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
     // the next chunk's loads (chosen with uniform selects, never a branch, so the compiler's
     // wait counts stay exact) are in flight while the current chunk is computed and while a
     // finished piece is written out.
+    // FUSE: the new K / V row of every pair whose last chunk lies in this wave's range, written
+    // to the pool before the range's first chunk load. The lanes that write a row, (lg, lc) with
+    // 4 lg <= slot % 16 < 4 lg + 4 (the row's place in its 16-token tile, as the block table
+    // places position context_len - 1), are the lanes that load it back in load_chunk, at the
+    // same bytes (dims (D / 16) lc ..), so the wave's own program order makes the later load see
+    // the row. No other wave reads the slot: the pair's last chunk, the only one holding the
+    // new position, is in this range alone, and a batch's new slots are private to their
+    // sequences. The first two pairs' rows are requested before the block-table and q loads
+    // (their wait then overlaps those loads), stored after them; further pairs (short contexts)
+    // two at a time after that.
+    struct NewRows {
+        int b, g, slot[2], pb[2], pg[2];
+        bool pv[2], more;
+        int64_t first;
+        int nch;
+        Ld kr[2], vr[2];
+    };
+    auto new_rows_load = [&](NewRows& nr) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            nr.pv[i] = nr.more;
+            nr.pb[i] = nr.b;
+            nr.pg[i] = nr.g;
+            if (nr.more) {  // on to the next pair in the flattened order (sequences with chunks)
+                nr.first += nr.nch;
+                if (++nr.g == kv_heads) {
+                    nr.g = 0;
+                    do {
+                        nr.b++;
+                    } while (nr.b < batch && pre[nr.b + 1] == pre[nr.b]);
+                }
+                if (nr.b < batch) {
+                    nr.nch = pre[nr.b + 1] - pre[nr.b];
+                    nr.more = nr.first + nr.nch - 1 < hi;
+                } else {
+                    nr.more = false;
+                }
+            }
+        }
+        const T* kn = static_cast<const T*>(ws.k_new);
+        const T* vn = static_cast<const T*>(ws.v_new);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            nr.slot[i] = nr.pv[i] ? ws.new_slots[nr.pb[i]] : -1;
+            if (nr.pv[i]) {
+                const int64_t src = (int64_t)nr.pb[i] * ws.new_st + (int64_t)nr.pg[i] * ws.new_sh +
+                                    (D / 16) * lc;
+                nr.kr[i] = *reinterpret_cast<const Ld*>(kn + src);
+                nr.vr[i] = *reinterpret_cast<const Ld*>(vn + src);
+            }
+        }
+    };
+    auto new_rows_store = [&](const NewRows& nr) {
+        T* const kpw = const_cast<T*>(k_pool);
+        T* const vpw = const_cast<T*>(v_pool);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int sl = nr.slot[i];
+            if (nr.pv[i] && sl >= 0 && sl < num_slots && lg == ((sl & 15) >> 2)) {
+                const int64_t dst = ((int64_t)nr.pg[i] * num_slots + sl) * D + (D / 16) * lc;
+                *reinterpret_cast<Ld*>(kpw + dst) = nr.kr[i];
+                *reinterpret_cast<Ld*>(vpw + dst) = nr.vr[i];
+            }
+        }
+    };
+
     Seg cur = seg_at(lo);
+    NewRows nr{};
+    if constexpr (FUSE) {
+        nr.b = cur.b;
+        nr.g = cur.g;
+        nr.nch = cur.nch;
+        nr.first = lo - cur.cb;  // flattened position of pair (b, g)'s first chunk
+        nr.more = nr.first + nr.nch - 1 < hi;
+        new_rows_load(nr);
+    }
     Slots cur_slots = seg_slots(cur);
     int64_t nx = lo + (cur.ce - cur.cb);
     bool has_nxt = nx < hi;
@@ -490,6 +578,16 @@ __global__ __launch_bounds__(64, 2) void paged_decode_mfma_kernel(
             nxt_slots = nn_slots;
         }
     };
+
+
+    if constexpr (FUSE) {
+        new_rows_store(nr);
+        while (nr.more) {
+            new_rows_load(nr);
+            new_rows_store(nr);
+        }
+        asm volatile("" ::: "memory");  // the stores stay before the chunk loads
+    }
 
     using pf_on = std::integral_constant<bool, true>;
     using pf_off = std::integral_constant<bool, false>;
@@ -636,8 +734,14 @@ static int launch_decode_mfma_d(void* out, const void* q, const void* k_pool, co
                                 int64_t num_slots, int max_ctx, float scale, int nwg, DecodeWs ws,
                                 hipStream_t stream) {
     const size_t lds = (size_t)(batch + 1) * sizeof(int);
-    auto kern = block_size == 16 ? paged_decode_mfma_kernel<T, TO, true, D>
-                                 : paged_decode_mfma_kernel<T, TO, false, D>;
+    const bool fuse = ws.k_new != nullptr;
+    if (fuse && block_size != 16) {  // paged_decode_write_kv takes 16-token pages only
+        set_error("paged_decode: the fused KV write needs 16-token pages");
+        return FLOUR_ERR_UNSUPPORTED;
+    }
+    auto kern = block_size == 16 ? (fuse ? paged_decode_mfma_kernel<T, TO, true, D, true>
+                                         : paged_decode_mfma_kernel<T, TO, true, D, false>)
+                                 : paged_decode_mfma_kernel<T, TO, false, D, false>;
     kern<<<dim3(nwg), dim3(64), lds, stream>>>(
         static_cast<TO*>(out), static_cast<const T*>(q), static_cast<const T*>(k_pool),
         static_cast<const T*>(v_pool), bt, max_blocks, ctx_lens, batch, num_heads, kv_heads, n_rep,
@@ -708,7 +812,7 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
                              int num_heads, int kv_heads, int head_dim, int block_size,
                              int64_t num_slots, int max_context_len, float scale, int dtype,
                              void* workspace, size_t workspace_bytes, bool ws_from_scratch,
-                             const int32_t* rows, void* stream);
+                             const int32_t* rows, const DecodeWs* fused, void* stream);
 
 // ------------------------------------------------------------------ allocation-free variant
 // The split-context workspace of flour_hip_paged_decode_noalloc lives in this file-scope device
@@ -760,7 +864,7 @@ extern "C" int flour_hip_paged_decode(void* out, int out_dtype, const void* q,
     return flour::paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables,
                                     max_blocks_per_seq, context_lens, batch, num_heads, kv_heads,
                                     head_dim, block_size, num_slots, max_context_len, scale, dtype,
-                                    workspace, workspace_bytes, false, nullptr, stream);
+                                    workspace, workspace_bytes, false, nullptr, nullptr, stream);
 }
 
 extern "C" size_t flour_hip_paged_decode_noalloc_max_workspace(void) {
@@ -780,7 +884,7 @@ extern "C" int flour_hip_paged_decode_noalloc(void* out, int out_dtype, const vo
     return flour::paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables,
                                     max_blocks_per_seq, context_lens, batch, num_heads, kv_heads,
                                     head_dim, block_size, num_slots, max_context_len, scale, dtype,
-                                    nullptr, 0, true, nullptr, stream);
+                                    nullptr, 0, true, nullptr, nullptr, stream);
 }
 
 namespace flour {
@@ -801,7 +905,7 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
                              int num_heads, int kv_heads, int head_dim, int block_size,
                              int64_t num_slots, int max_context_len, float scale, int dtype,
                              void* workspace, size_t workspace_bytes, bool ws_from_scratch,
-                             const int32_t* rows, void* stream) {
+                             const int32_t* rows, const DecodeWs* fused, void* stream) {
     if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) {
         set_error("paged_decode: unknown dtype (%d, out %d)", dtype, out_dtype);
         return FLOUR_ERR_INVALID_ARGUMENT;
@@ -825,8 +929,8 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
     const int n_rep = num_heads / kv_heads;
     const bool mfma = decode_mfma_supported(dtype, head_dim, block_size, n_rep, batch, num_heads,
                                             num_slots, q, k_pool, v_pool);
-    if (!mfma && rows) {
-        set_error("paged_decode: row indices need the matrix-core path");
+    if (!mfma && (rows || fused)) {
+        set_error("paged_decode: row indices and the fused KV write need the matrix-core path");
         return FLOUR_ERR_UNSUPPORTED;
     }
     if (!mfma) {
@@ -871,6 +975,11 @@ static int paged_decode_impl(void* out, int out_dtype, const void* q, const void
         reinterpret_cast<char*>(ws.o) +
         align256((size_t)2 * nwg * n_rep * (size_t)head_dim * sizeof(float)));
     ws.rows = rows;
+    ws.k_new = fused ? fused->k_new : nullptr;
+    ws.v_new = fused ? fused->v_new : nullptr;
+    ws.new_st = fused ? fused->new_st : 0;
+    ws.new_sh = fused ? fused->new_sh : 0;
+    ws.new_slots = fused ? fused->new_slots : nullptr;
 #define FLOUR_DEC(T)                                                                            \
     do {                                                                                        \
         if (out_dtype == FLOUR_DTYPE_F32)                                                       \
@@ -915,7 +1024,40 @@ int paged_decode_rows(void* out, int out_dtype, const void* q, const void* k_poo
     return paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables, max_blocks_per_seq,
                              context_lens, batch, num_heads, kv_heads, head_dim, block_size,
                              num_slots, max_context_len, scale, dtype, workspace, workspace_bytes,
-                             false, rows, stream);
+                             false, rows, nullptr, stream);
+}
+
+int paged_decode_write_kv(void* out, int out_dtype, const void* q, void* k_pool, void* v_pool,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          const int32_t* context_lens, int batch, int num_heads, int kv_heads,
+                          int head_dim, int block_size, int64_t num_slots, int max_context_len,
+                          float scale, int dtype, void* workspace, size_t workspace_bytes,
+                          const void* k_new, const void* v_new, int64_t new_stride_tok,
+                          int64_t new_stride_head, const int32_t* new_slots, void* stream) {
+    const int es = (dtype == FLOUR_DTYPE_F32) ? 4 : 2;
+    const uint64_t row_align = head_dim == 128 ? 16 : 8;  // a lane's share of a row
+    // 16-token pages only: the fused instantiation for other page sizes spills registers in its
+    // piece epilogue (a reload there waits for every chunk load in flight)
+    if (!k_new || !v_new || !new_slots || batch < 1 || kv_heads <= 0 || block_size != 16 ||
+        num_heads % kv_heads != 0 ||
+        !decode_mfma_supported(dtype, head_dim, block_size, num_heads / kv_heads, batch,
+                               num_heads, num_slots, q, k_pool, v_pool) ||
+        (((uint64_t)(uintptr_t)k_new | (uint64_t)(uintptr_t)v_new |
+          (uint64_t)(new_stride_tok * es) | (uint64_t)(new_stride_head * es)) &
+         (row_align - 1)) != 0) {
+        set_error("paged_decode_write_kv: shape not taken by the fused launch");
+        return FLOUR_ERR_UNSUPPORTED;
+    }
+    DecodeWs fz{};
+    fz.k_new = k_new;
+    fz.v_new = v_new;
+    fz.new_st = new_stride_tok;
+    fz.new_sh = new_stride_head;
+    fz.new_slots = new_slots;
+    return paged_decode_impl(out, out_dtype, q, k_pool, v_pool, block_tables, max_blocks_per_seq,
+                             context_lens, batch, num_heads, kv_heads, head_dim, block_size,
+                             num_slots, max_context_len, scale, dtype, workspace, workspace_bytes,
+                             false, nullptr, &fz, stream);
 }
 
 }  // namespace flour

@@ -428,6 +428,24 @@ class KvBatch:
                                              out.stride(1), float(scale), _stream()))
         return out
 
+    def write_kv_attention(self, layer: int, k, v, q, scale: float, out=None, out_dtype=None):
+        """``write_kv(layer, k, v)`` then ``attention(layer, q, scale)`` in one call; a decode
+        step over private tail blocks runs as one launch (the decode kernel writes the new rows
+        before it reads them). k / v packed (rows, kv_heads, head_dim) with a unit last stride,
+        q (rows, num_heads, head_dim); returns the attention output."""
+        import torch
+        from .ops import _ptr, _stream, dtype_code
+
+        assert k.stride() == v.stride() and k.dtype == v.dtype == self.dtype and k.stride(2) == 1
+        T, H, D = q.shape
+        if out is None:
+            out = torch.empty((T, H, D), dtype=out_dtype or q.dtype, device=q.device)
+        check(lib().flour_kv_batch_write_kv_attention(
+            self._h, layer, _ptr(k), _ptr(v), k.stride(0), k.stride(1), _ptr(q), H, q.stride(0),
+            q.stride(1), _ptr(out), dtype_code(out.dtype), out.stride(0), out.stride(1),
+            float(scale), _stream()))
+        return out
+
     def pool(self, layer: int):
         """(k_pool, v_pool) of a layer as torch views (kv_heads, num_slots, head_dim)."""
         k, v, ns = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int64()

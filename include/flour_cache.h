@@ -226,6 +226,21 @@ int flour_kv_batch_attention(flour_kv_batch* b, int layer, const void* q, int nu
                              int64_t q_stride_tok, int64_t q_stride_head, void* out,
                              int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,
                              float scale, void* stream);
+/* flour_kv_batch_write_kv followed by flour_kv_batch_attention, as one call: the order of the
+ * reference's layer (Cache::write_kv, cache.rs:451-453, then paged_attention, cpu.rs:57-112).
+ * A decode step (every sequence brings one row) with packed contiguous q and out over 16-bit
+ * pools of 16-token blocks at head_dim 128 or 64, whose new positions sit in blocks no other
+ * sequence or the prefix registry holds, runs as ONE launch: the decode kernel writes each new K / V row into
+ * the pool before it attends to it (the same pools and output as the two calls, bit for bit).
+ * Every other step runs the two calls. This entry point has no counterpart in the reference; it
+ * is for the per-layer loop of a continuous-batching server, where the KV write of a decode
+ * step's few rows costs a whole launch. */
+int flour_kv_batch_write_kv_attention(flour_kv_batch* b, int layer, const void* k,
+                                      const void* v, int64_t kv_stride_tok,
+                                      int64_t kv_stride_head, const void* q, int num_heads,
+                                      int64_t q_stride_tok, int64_t q_stride_head, void* out,
+                                      int out_dtype, int64_t o_stride_tok, int64_t o_stride_head,
+                                      float scale, void* stream);
 int flour_kv_batch_pool(const flour_kv_batch* b, int layer, void** k_pool, void** v_pool,
                         int64_t* num_slots);
 

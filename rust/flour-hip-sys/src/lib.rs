@@ -187,6 +187,11 @@ extern "C" {
         num_heads: c_int, q_stride_tok: i64, q_stride_head: i64, out: *mut c_void,
         out_dtype: c_int, o_stride_tok: i64, o_stride_head: i64, scale: f32,
         stream: *mut c_void) -> c_int;
+    pub fn flour_kv_batch_write_kv_attention(b: *mut FlourKvBatch, layer: c_int,
+        k: *const c_void, v: *const c_void, kv_stride_tok: i64, kv_stride_head: i64,
+        q: *const c_void, num_heads: c_int, q_stride_tok: i64, q_stride_head: i64,
+        out: *mut c_void, out_dtype: c_int, o_stride_tok: i64, o_stride_head: i64, scale: f32,
+        stream: *mut c_void) -> c_int;
     pub fn flour_kv_batch_pool(b: *const FlourKvBatch, layer: c_int, k_pool: *mut *mut c_void,
         v_pool: *mut *mut c_void, num_slots: *mut i64) -> c_int;
 }

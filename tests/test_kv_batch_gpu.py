@@ -246,3 +246,84 @@ def test_mixed_step_runs_decode_rows_on_the_decode_kernel(device):
                                torch.tensor(bt[pi], device=device), max(qn), SCALE,
                                block_size=BS, out_dtype=torch.float32)
     assert torch.equal(split[p_rows], p_out)
+
+
+@pytest.mark.parametrize("Hq,Gk,Dh,bs", [(32, 8, 128, 16), (14, 2, 64, 16), (16, 4, 128, 32)])
+def test_fused_write_and_decode_equals_two_launches(device, Hq, Gk, Dh, bs):
+    """flour_kv_batch_write_kv_attention on a decode step: the decode kernel writes each new K / V
+    row into the pool before it attends to it, in one launch. Output (fp32 and bf16) and both
+    pools bit-identical to the KV write followed by the attention (the switch set to two
+    launches), and the output against the oracle. Contexts put the new position at every place
+    of its 16-token tile (1 .. 48 tokens) next to long ones (U[512, 3000]), so workgroup ranges
+    start and end inside, at and past a pair's last chunk. 32-token pages take the two launches
+    (the fused instantiation is built for 16-token pages) and must give the same."""
+    rng = np.random.default_rng(Dh + bs)
+    b = KvBatch(1, 12000 // (bs // 16), 64, 3072, 64 * 3072, Hq, Gk, Dh, torch.bfloat16, bs)
+    ctx = list(range(1, 49)) + [int(x) for x in rng.integers(512, 3001, size=16)]
+    sids = [b.add_sequence() for _ in ctx]
+    _fill(b, [s for s, c in zip(sids, ctx) if c > 1], [c - 1 for c in ctx if c > 1], 0, 11)
+    b.step(sids, [1] * len(sids))
+    assert [b.len(s) for s in sids] == ctx
+    n = len(sids)
+    gd = torch.Generator(device="cuda").manual_seed(12)
+    k = torch.randn((n, Gk, Dh), generator=gd, device="cuda").to(torch.bfloat16)
+    v = torch.randn((n, Gk, Dh), generator=gd, device="cuda").to(torch.bfloat16)
+    q = torch.randn((n, Hq, Dh), generator=gd, device="cuda").to(torch.bfloat16)
+    kp, vp = b.pool(0)
+    kp0, vp0 = kp.clone(), vp.clone()
+
+    def run(fuse, out_dtype):
+        kp.copy_(kp0)
+        vp.copy_(vp0)
+        assert _lib.lib().flour_hip_set_batch_fuse(fuse) == 0
+        try:
+            out = b.write_kv_attention(0, k, v, q, SCALE, out_dtype=out_dtype)
+        finally:
+            _lib.lib().flour_hip_set_batch_fuse(1)
+        torch.cuda.synchronize()
+        return out, kp.clone(), vp.clone()
+
+    for od in (torch.float32, torch.bfloat16):
+        f_out, f_k, f_v = run(1, od)
+        u_out, u_k, u_v = run(0, od)
+        assert torch.equal(f_k, u_k) and torch.equal(f_v, u_v)
+        assert not torch.equal(f_k, kp0)  # the new rows were written
+        assert torch.equal(f_out, u_out)
+    f_out, _, _ = run(1, torch.float32)
+    mb = max(len(b.blocks(s)) for s in sids)
+    bt = np.zeros((n, mb), np.int32)
+    for i, s in enumerate(sids):
+        bl = b.blocks(s)
+        bt[i, :len(bl)] = bl
+    cu = np.arange(n + 1, dtype=np.int32)
+    kl = np.array([b.len(s) for s in sids], np.int32)
+    ref = O.paged_attention(to_np(q), to_np(kp), to_np(vp), bt, cu, kl, bs, SCALE, bf16=True)
+    max_abs, rel = errors(to_np(f_out), ref)
+    print(f"fused write + decode H={Hq} G={Gk} D={Dh} bs={bs}: max_abs={max_abs:.3e} "
+          f"rel_l2={rel:.3e}", flush=True)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
+def test_fused_entry_point_runs_other_steps_as_two_calls(device):
+    """A mixed step (and a prefill step) through flour_kv_batch_write_kv_attention takes the
+    KV write and the attention as two calls: the same pools and output as calling them."""
+    g = torch.Generator(device="cpu").manual_seed(13)
+    b = make()
+    sids = [b.add_sequence() for _ in range(3)]
+    for qn in ([40, 7, 1], [1, 1, 5]):
+        b.step(sids, qn)
+        T = sum(qn)
+        k, v = rows(T, g), rows(T, g)
+        q = torch.randn((T, H, D), generator=g).to(torch.bfloat16).cuda()
+        kp, vp = b.pool(0)
+        kp0, vp0 = kp.clone(), vp.clone()
+        out = b.write_kv_attention(0, k, v, q, SCALE, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        k1, v1 = kp.clone(), vp.clone()
+        kp.copy_(kp0)
+        vp.copy_(vp0)
+        b.write_kv(0, k, v)
+        ref = b.attention(0, q, SCALE, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(kp, k1) and torch.equal(vp, v1) and torch.equal(out, ref)
+        check(b, 0, sids, qn, q, out, f"write + attention in one call, rows {qn}")
