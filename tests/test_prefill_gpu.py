@@ -12,6 +12,8 @@ max |reference|, and finite exactly where the reference is.
 """
 from __future__ import annotations
 
+import time
+
 import numpy as np
 import pytest
 import torch
@@ -297,16 +299,14 @@ def test_prefill_f16_pools(device):
 
 def test_prefill_long_sequence_many_tiles(device):
     """One 4100-row sequence (33 query tiles, 65 kv tiles for the last) next to a 1-row one;
-    the oracle checks the first and last rows of the long sequence and the short one."""
+    the oracle checks every row of both."""
     c = make_prefill(2, 8, 2, 128, 16, (1, 1), prefix=0, dtype=torch.bfloat16, seed=31,
                      device=device, q_lens=[4100, 1])
     write(c)
     out = to_np(run(c, torch.float32))
     cu = to_np(c.cu_seqlens_q)
-    # rows of the long sequence: the oracle runs on the whole sequence, compare a sample
     ref, rows = oracle_prefill(c, seqs=[0])
-    pick = np.r_[0:64, 2000:2064, 4036:4100]
-    max_abs, rel = errors(out[rows][pick], ref[pick])
+    max_abs, rel = errors(out[rows], ref)
     print(f"long fp32-out max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
     ref1, rows1 = oracle_prefill(c, seqs=[1])
@@ -591,8 +591,8 @@ def test_prefill_dma_staging_matches_register_staging(device, case):
 
 def test_prefill_long_workload_dma_staging(device):
     """The long-prompt workload (2 x 8,192 rows, Llama-3-8B heads) takes direct-to-LDS staging
-    by default: bit-identical to register staging, and its last 128 rows of sequence 1 (a
-    suffix over 8,064 earlier positions) against the oracle."""
+    by default: bit-identical to register staging, and every row of the batch against the
+    oracle (~1.1 TFLOP of causal attention on the host cores)."""
     from flour_amd import _lib
     c = make_workload("prefill_bf16_long_llama3_8b", device=device)
     write(c)
@@ -614,13 +614,13 @@ def test_prefill_long_workload_dma_staging(device):
     assert ws.buf.numel() >= ops.prefill_workspace_bytes(2, c.block_tables.shape[1],
                                                          c.block_size, 8, 128, c.q.dtype) > 0
     assert torch.equal(a, b)
-    cu = to_np(c.cu_seqlens_q)
-    rows = np.arange(int(cu[2]) - 128, int(cu[2]))
-    ref = O.paged_attention(to_np(c.q)[rows], to_np(c.k_pool), to_np(c.v_pool),
-                            to_np(c.block_tables)[1:2], np.array([0, 128], dtype=np.int32),
-                            to_np(c.kv_lens)[1:2], c.block_size, c.scale, bf16=True)
-    max_abs, rel = errors(to_np(a)[rows], ref)
-    print(f"long workload last rows max_abs={max_abs:.3e} rel_l2={rel:.3e}", flush=True)
+    t0 = time.perf_counter()
+    ref = O.paged_attention(to_np(c.q), to_np(c.k_pool), to_np(c.v_pool), to_np(c.block_tables),
+                            to_np(c.cu_seqlens_q), to_np(c.kv_lens), c.block_size, c.scale,
+                            bf16=True)
+    max_abs, rel = errors(to_np(a), ref)
+    print(f"long workload, all rows: max_abs={max_abs:.3e} rel_l2={rel:.3e} "
+          f"(oracle {time.perf_counter() - t0:.1f} s)", flush=True)
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
