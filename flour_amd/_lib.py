@@ -160,6 +160,7 @@ def lib() -> ctypes.CDLL:
 EXTRA_SIGNATURES: dict[str, tuple] = {
     "flour_hip_set_prefill_precise_p": (_c_int, [_c_int]),
     "flour_hip_set_decode_workgroups": (_c_int, [_c_int]),
+    "flour_hip_set_decode_xcd_weight": (_c_int, [_c_int]),
     "flour_hip_set_prefill_persistent": (_c_int, [_c_int]),
     "flour_hip_set_prefill_dma": (_c_int, [_c_int]),
     "flour_hip_set_batch_split": (_c_int, [_c_int]),

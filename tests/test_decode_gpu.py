@@ -129,19 +129,24 @@ def test_decode_repeat_calls_reuse_workspace(device):
     assert torch.equal(a, b) and torch.equal(s1, s2)
 
 
+@pytest.mark.parametrize("w", [0, 2, 16])
 @pytest.mark.parametrize("nwg", [1, 3, 7, 100, 513, 4096])
-def test_decode_workgroup_partitions_agree(device, nwg):
-    """Any number of workgroups (hence any cut of the chunk list into pieces, including more
-    workgroups than chunks) meets the same fp32-accumulator bound."""
+def test_decode_workgroup_partitions_agree(device, nwg, w):
+    """Any number of workgroups and any weighting of the ranges between even and odd workgroups
+    (hence any cut of the chunk list into pieces, including more workgroups than chunks and
+    empty ranges) meets the same fp32-accumulator bound."""
     from flour_amd import _lib
     c = make_decode(6, 32, 8, 128, 16, (1, 5000), dtype=torch.bfloat16, seed=23, device=device,
                     context_lens=[4999, 1, 0, 33, 2048, 700])
     ref = oracle_decode(c)
-    assert _lib.lib().flour_hip_set_decode_workgroups(nwg) == 0
+    lib = _lib.lib()
+    assert lib.flour_hip_set_decode_workgroups(nwg) == 0
+    assert lib.flour_hip_set_decode_xcd_weight(w) == 0
     try:
         got = to_np(run(c, torch.float32))
     finally:
-        _lib.lib().flour_hip_set_decode_workgroups(0)
+        lib.flour_hip_set_decode_workgroups(0)
+        lib.flour_hip_set_decode_xcd_weight(2)
     max_abs, rel = errors(got, ref)
     assert max_abs <= 2e-3 and rel <= 1e-3
     assert not got[2].any()  # empty context
