@@ -283,21 +283,31 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         const int cap = n_rep <= 4 ? 2 : 3;
         return min(r <= 32 ? 3 : 2, cap);
     };
-    // shape of tile qt of sequence sq (its last tile by its rows, the others 2 heads x 128)
-    auto tile_lg = [&](int sq, int qt, int t) {
-        return qt < t - 1 ? 1 : shape_lg(sched_cu[sq + 1] - sched_cu[sq] - PF_QT * qt);
+    // Entry (sequence sq, tile qt = NQ-1-L): what the schedule needs of it, read from LDS once.
+    // Its items: with an odd n_rep the last head of tiles of 2 heads x 128 is a one-head item,
+    // tiles 2j and 2j + 1 sharing one of 256 rows that costs about as much as a two-head item of
+    // tile 2j + 1. Part 1 (c1): the multi-head items, then at odd qt the shared one-head items;
+    // part 2 (c2): one-head items of a single tile (2j without tile 2j + 1).
+    struct Entry {
+        int seq, qt, L, lg, c0, ql, kvl, c1, c2;
     };
-    // items of entry (sq, qt). With an odd n_rep the last head of tiles of 2 heads x 128 is a
-    // one-head item, tiles 2j and 2j + 1 sharing one of 256 rows that costs about as much as
-    // a two-head item of tile 2j + 1. Part 1: the multi-head items, then at odd qt the shared
-    // one-head items; part 2: one-head items of a single tile (2j without tile 2j + 1).
-    auto entry_items = [&](int sq, int qt, int& c1, int& c2) {
-        const int t = seq_tiles(sq);
-        const int lg = tile_lg(sq, qt, t);
-        const bool lone = (n_rep & 1) && lg == 1;
-        c1 = kv_heads * (lg == 1 ? (n_rep >> 1) : ((n_rep + (1 << lg) - 1) >> lg)) +
-             (lone && (qt & 1) ? kv_heads : 0);
-        c2 = lone && !(qt & 1) && !(qt + 1 < t && tile_lg(sq, qt + 1, t) == 1) ? kv_heads : 0;
+    auto entry_at = [&](int sq, int L) __attribute__((always_inline)) {
+        Entry x;
+        x.seq = sq;
+        x.L = L;
+        x.qt = NQ - 1 - L;
+        x.c0 = sched_cu[sq];
+        x.ql = sched_cu[sq + 1] - x.c0;
+        x.kvl = sched_kv[sq];
+        const int t = x.ql <= 0 ? 0 : min((x.ql + PF_QT - 1) / PF_QT, NQ);  // as seq_tiles
+        // shape of tile qt: its last tile by its rows, the others 2 heads x 128
+        auto lg_of = [&](int qt) { return qt < t - 1 ? 1 : shape_lg(x.ql - PF_QT * qt); };
+        x.lg = lg_of(x.qt);
+        const bool lone = (n_rep & 1) && x.lg == 1;
+        x.c1 = kv_heads * (x.lg == 1 ? (n_rep >> 1) : ((n_rep + (1 << x.lg) - 1) >> x.lg)) +
+               (lone && (x.qt & 1) ? kv_heads : 0);
+        x.c2 = lone && !(x.qt & 1) && !(x.qt + 1 < t && lg_of(x.qt + 1) == 1) ? kv_heads : 0;
+        return x;
     };
     int total_items = 0, total_base = 0, total1 = 0;  // items; (level, sequence) pairs; part 1
     bool flex_on = false;
@@ -343,6 +353,22 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         // causal kv tiles; none when kv_len < q_len (the rows are written as zeros)
         e[7] = (ok && kvl >= ql) ? (kvl - ql + row_last + 1 + PF_KT - 1) / PF_KT : 0;
         return ok;
+    };
+    // item k of this workgroup from an Entry: the entry's tile, or tile qt - 1 for a one-head item
+    // of 256 rows (level L + 1); fields as put_item writes them
+    auto put_item_e = [&](int k, const Entry& x, int level, int kvh, int h0, int lg)
+                          __attribute__((always_inline)) {
+        const int qt = NQ - 1 - level;
+        const int row_last = min(qt * PF_QT + (256 >> lg), x.ql) - 1;
+        int* e = sched_items[k];
+        e[0] = x.seq;
+        e[1] = qt;
+        e[2] = kvh;
+        e[3] = h0 | (lg << 16);
+        e[4] = q_rows ? q_rows[x.seq] : x.c0;
+        e[5] = x.ql;
+        e[6] = x.kvl;
+        e[7] = x.kvl >= x.ql ? (x.kvl - x.ql + row_last + 1 + PF_KT - 1) / PF_KT : 0;
     };
     if (persistent) {
         for (int i = tid; i <= num_seqs; i += PF_THREADS) sched_cu[i] = cu_seqlens[i];
@@ -406,12 +432,13 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             }
             const int L0 = L, i0 = e0 - sched_cum[L];
             int s1 = 0, s2 = 0;
+            Entry x0{};  // this thread's first entry, kept for the second walk
             for (int e = e0, i = i0; e < e1; e++) {
-                int c1, c2;
-                entry_items(sched_order[i], NQ - 1 - L, c1, c2);
-                s1 += c1;
-                s2 += c2;
-                if (++i == sched_more[NQ - 1 - L]) {  // levels are never empty once started
+                const Entry x = entry_at(sched_order[i], L);
+                if (e == e0) x0 = x;
+                s1 += x.c1;
+                s2 += x.c2;
+                if (++i == sched_more[x.qt]) {  // levels are never empty once started
                     L++;
                     i = 0;
                 }
@@ -436,30 +463,29 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             total_items = total1 + __builtin_amdgcn_readfirstlane(t2);
             // this run's first item of part 1 and of part 2, as list indices
             const int a1_0 = b1 + x1 - s1, a2_0 = total1 + b2 + x2 - s2;
-            // walks this thread's entries: fn(seq, qt, L, first item and count of part 1, of part 2)
+            // walks this thread's entries: fn(entry, first item of part 1, of part 2)
             auto walk = [&](auto&& fn) {
                 int L = L0, a1 = a1_0, a2 = a2_0;
                 for (int e = e0, i = i0; e < e1; e++) {
-                    const int seq = sched_order[i], qt = NQ - 1 - L;
-                    int c1, c2;
-                    entry_items(seq, qt, c1, c2);
-                    fn(seq, qt, L, a1, c1, a2, c2);
-                    a1 += c1;
-                    a2 += c2;
-                    if (++i == sched_more[qt]) {  // levels are never empty once started
+                    const Entry x = e == e0 ? x0 : entry_at(sched_order[i], L);
+                    fn(x, a1, a2);
+                    a1 += x.c1;
+                    a2 += x.c2;
+                    if (++i == sched_more[x.qt]) {  // levels are never empty once started
                         L++;
                         i = 0;
                     }
                 }
             };
-            // item p of part `part` of entry (seq, tile qt on level L), into slot k
-            auto put_entry_item = [&](int k, int part, int p, int seq, int qt, int L) {
+            // item p of part `part` of entry x, into slot k
+            auto put_entry_item = [&](int k, int part, int p, const Entry& x) {
+                const int L = x.L;
                 int level = L, kvh, h0, lg = 1;
                 if (part) {
                     kvh = p;
                     h0 = n_rep - 1;
                 } else {
-                    lg = tile_lg(seq, qt, seq_tiles(seq));
+                    lg = x.lg;
                     if (lg == 1 && p >= kv_heads * half_rep) {  // 1 head x 256 rows from qt - 1
                         kvh = p - kv_heads * half_rep;
                         h0 = n_rep - 1;
@@ -474,7 +500,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                         h0 = (p - kvh * g) << lg;
                     }
                 }
-                put_item(k, seq, level, kvh, h0, lg);
+                put_item_e(k, x, level, kvh, h0, lg);
             };
             // Rounds 0 .. R-2 follow the snake: item idx of round rd = idx / G goes to workgroup
             // idx % G on even rounds, G-1 - idx % G on odd ones. From three rounds on, the last
@@ -487,34 +513,33 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
             const bool ranked = rounds >= 3 && rounds <= PF_MAX_WG_ITEMS && G <= PF_MAX_GRID;
             const int cut = ranked ? (rounds - 1) * G : total_items;
             wg_items = ranked ? rounds - 1 : items_of_wg(total_items);
-            walk([&](int seq, int qt, int L, int a1, int c1, int a2, int c2) {
+            walk([&](const Entry& x, int a1, int a2) {
 #pragma unroll
                 for (int part = 0; part < 2; part++) {
-                    const int a = part ? a2 : a1, c = part ? c2 : c1;
+                    const int a = part ? a2 : a1, c = part ? x.c2 : x.c1;
                     for (int rd = a / G; rd * G < a + c && rd < wg_items; rd++) {
                         const int idx = rd * G + ((rd & 1) ? G - 1 - wg : wg);
-                        if (idx >= a && idx < a + c) put_entry_item(rd, part, idx - a, seq, qt, L);
+                        if (idx >= a && idx < a + c) put_entry_item(rd, part, idx - a, x);
                     }
                 }
                 if (!ranked) return;
                 // the entry's items of the last round, for the workgroup that ranks there
 #pragma unroll
                 for (int part = 0; part < 2; part++) {
-                    const int a = part ? a2 : a1, end = a + (part ? c2 : c1);
+                    const int a = part ? a2 : a1, end = a + (part ? x.c2 : x.c1);
                     for (int idx = max(a, cut); idx < end; idx++)
-                        sched_last[idx - cut] = int2{seq | (L << 11) | (part << 20), idx - a};
+                        sched_last[idx - cut] = int2{x.seq | (x.L << 11) | (part << 20), idx - a};
                 }
                 // the entry's items before the cut add their cost to the workgroups the snake
                 // gives them: per round one contiguous range of workgroups, as differences. All
                 // items of an entry share its kv tile count (a one-head item of tiles qt - 1 and
                 // qt ends on tile qt's last row).
-                const int ql = sched_cu[seq + 1] - sched_cu[seq], kvl = sched_kv[seq];
-                const int row_end = min((qt + 1) * PF_QT, ql);
-                const int n_kt = kvl >= ql ? (kvl - ql + row_end + PF_KT - 1) / PF_KT : 0;
+                const int row_end = min((x.qt + 1) * PF_QT, x.ql);
+                const int n_kt = x.kvl >= x.ql ? (x.kvl - x.ql + row_end + PF_KT - 1) / PF_KT : 0;
                 const int cost = PF_COST_TILE * n_kt + PF_COST_ITEM;
 #pragma unroll
                 for (int part = 0; part < 2; part++) {
-                    const int a = part ? a2 : a1, end = min(a + (part ? c2 : c1), cut);
+                    const int a = part ? a2 : a1, end = min(a + (part ? x.c2 : x.c1), cut);
                     for (int rd = a / G; rd * G < end; rd++) {
                         const int p0 = max(a, rd * G) - rd * G, p1 = min(end, rd * G + G) - rd * G;
                         atomicAdd(&sched_load[(rd & 1) ? G - p1 : p0], cost);
@@ -552,8 +577,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                     wg_items = rounds;
                     if (tid == 0) {
                         const int2 d = sched_last[rank];
-                        const int L = (d.x >> 11) & 511;
-                        put_entry_item(rounds - 1, d.x >> 20, d.y, d.x & 2047, NQ - 1 - L, L);
+                        put_entry_item(rounds - 1, d.x >> 20, d.y,
+                                       entry_at(d.x & 2047, (d.x >> 11) & 511));
                     }
                 }
             }
