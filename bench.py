@@ -485,9 +485,12 @@ def prefill_kernel_name(case) -> str:
     """The kernel a prefill workload runs on (the dispatch rule of flour_hip_varlen_prefill)."""
     import torch
 
-    mfma = (case.q.dtype in (torch.bfloat16, torch.float16) and case.q.shape[2] in (64, 128)
-            and case.block_size % 16 == 0)
-    return "varlen_prefill_mfma_kernel" if mfma else "attn_simt_kernel"
+    d = case.q.shape[2]
+    if case.q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128) and case.block_size % 16 == 0:
+        return "varlen_prefill_mfma_kernel"
+    if case.q.dtype == torch.float32 and d in (64, 128):
+        return "prefill_f32_mfma_kernel (fp32 matrix cores)"
+    return "attn_simt_kernel"
 
 
 def decode_kernel_name(case) -> str:

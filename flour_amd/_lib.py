@@ -163,6 +163,7 @@ EXTRA_SIGNATURES: dict[str, tuple] = {
     "flour_hip_set_decode_xcd_weight": (_c_int, [_c_int]),
     "flour_hip_set_prefill_persistent": (_c_int, [_c_int]),
     "flour_hip_set_prefill_dma": (_c_int, [_c_int]),
+    "flour_hip_set_prefill_f32_mfma": (_c_int, [_c_int]),
     "flour_hip_set_batch_split": (_c_int, [_c_int]),
     "flour_hip_set_batch_fuse": (_c_int, [_c_int]),
     "flour_hip_empty_launch": (_c_int, [_vp]),

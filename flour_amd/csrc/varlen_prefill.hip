@@ -46,6 +46,15 @@
 
 namespace flour {
 
+bool prefill_f32_mfma_supported(int dtype, int head_dim, int num_seqs, int max_seqlen_q,
+                                int block_size, int64_t num_slots);
+int launch_prefill_f32_mfma(int out_dtype, void* out, int64_t o_st, int64_t o_sh, const void* q,
+                            int64_t q_st, int64_t q_sh, const void* k_pool, const void* v_pool,
+                            const int32_t* cu_seqlens_q, const int32_t* q_rows,
+                            const int32_t* kv_lens, const int32_t* block_tables, int max_blocks,
+                            int num_seqs, int max_seqlen_q, int num_heads, int n_rep,
+                            int head_dim, int block_size, int64_t num_slots, float scale,
+                            hipStream_t stream);
 bool simt_supported(int dtype, int head_dim, const void* q, int64_t q_st, int64_t q_sh,
                     const void* k_pool, const void* v_pool);
 int launch_attn_simt(int dtype, int out_dtype, void* out, int64_t o_st, int64_t o_sh,
@@ -1724,6 +1733,14 @@ static int varlen_prefill_impl(void* out, int out_dtype, int64_t o_stride_tok,
     // (the Q rows of a wave are loaded with 32-bit offsets from its first row: 31 row strides)
     const bool mfma = aligned && prefill_mfma_supported(dtype, head_dim, block_size, num_slots,
                                                         scale, q_stride_tok);
+    // fp32 pools at head_dim 64 / 128: the fp32 matrix cores
+    if (!mfma && !q_rows && aligned &&
+        prefill_f32_mfma_supported(dtype, head_dim, num_seqs, max_seqlen_q, block_size, num_slots))
+        return launch_prefill_f32_mfma(out_dtype, out, o_stride_tok, o_stride_head, q, q_stride_tok,
+                                       q_stride_head, k_pool, v_pool, cu_seqlens_q, nullptr,
+                                       kv_lens, block_tables, max_blocks_per_seq, num_seqs,
+                                       max_seqlen_q, num_heads, n_rep, head_dim, block_size,
+                                       num_slots, scale, s);
     if (!mfma && q_rows) {
         set_error("varlen_prefill: row indices need the matrix-core path");
         return FLOUR_ERR_UNSUPPORTED;

@@ -208,7 +208,7 @@ def test_prefill_block_table_window_crossings(device, bs, kv):
 
 def test_prefill_kv_shorter_than_q_gives_zero_rows_on_every_path(device):
     """A sequence whose kv length is below its query count attends nothing: its rows are
-    written as zeros by the MFMA path (bf16 pools) and by the generic path (fp32 pools), as
+    written as zeros by the MFMA path (bf16 pools) and by the fp32 path (fp32 pools), as
     the oracle does; the other sequences are unaffected."""
     for dt in (torch.bfloat16, torch.float32):
         c = make_prefill(3, 8, 2, 128, 16, (1, 1), prefix=0, dtype=dt, seed=29, device=device,
@@ -714,11 +714,16 @@ def test_prefill_dma_switch_rejects_bad_mode():
 def test_prefill_vector_kernel_shapes(device, dt, H, G, D, bs, lens, prefix):
     """Shapes the matrix-core prefill does not take run on the vector kernel: fp32 max-abs
     <= 1e-5 against the oracle, 16-bit pools 2e-3 / 1e-3 (fp32 output)."""
+    from flour_amd import _lib
     c = make_prefill(len(lens), H, G, D, bs, (1, 1), prefix=prefix, dtype=dt, seed=H + D,
                      device=device, q_lens=lens)
     write(c)
     ref, rows = oracle_prefill(c)
-    got = to_np(run(c, torch.float32))[rows]
+    assert _lib.lib().flour_hip_set_prefill_f32_mfma(0) == 0  # fp32 at 64 / 128 too
+    try:
+        got = to_np(run(c, torch.float32))[rows]
+    finally:
+        _lib.lib().flour_hip_set_prefill_f32_mfma(1)
     max_abs, rel = errors(got, ref)
     print(f"vector prefill {dt} H={H} G={G} D={D}: max_abs={max_abs:.3e} rel={rel:.3e}", flush=True)
     if dt == torch.float32:
