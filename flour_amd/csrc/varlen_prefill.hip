@@ -385,43 +385,69 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
         if constexpr (FLEX)
             for (int i = tid; i <= G && G <= PF_MAX_GRID; i += PF_THREADS) sched_load[i] = 0;
         __syncthreads();
-        if (w == 0) {
-            // Wave 0 alone, without barriers (a wave's LDS operations complete in order):
-            // histogram of tile counts, more[v] = sequences with a tile count above v (its
-            // suffix sum), a stable counting sort by decreasing tile count, and the level
-            // offsets.
-            for (int v = lane; v <= NQ; v += 64) sched_fill[v] = 0;
-            __builtin_amdgcn_wave_barrier();
-            for (int sq = lane; sq < num_seqs; sq += 64) atomicAdd(&sched_fill[seq_tiles(sq)], 1);
-            __builtin_amdgcn_wave_barrier();
-            wave_scan(NQ + 1, [&](int v) { return sched_fill[v]; },
-                      [&](int v, int x) { sched_more[v] = x; }, true);
-            __builtin_amdgcn_wave_barrier();
-            for (int v = lane; v <= NQ; v += 64) sched_fill[v] = 0;
-            __builtin_amdgcn_wave_barrier();
-            // stable counting sort (every workgroup must build the same order): 64 sequences
-            // at a time, a lane's rank among equal tile counts comes from ballots over the
-            // count's bits (counts are at most PF_MAX_LEVELS < 1024)
-            for (int base = 0; base < num_seqs; base += 64) {
-                const int sq = base + lane;
-                const int n = sq < num_seqs ? seq_tiles(sq) : 0;
-                uint64_t same = ~0ull;
-#pragma unroll
-                for (int b = 0; b < 10; b++) {
-                    const uint64_t bal = __ballot((n >> b) & 1);
-                    same &= ((n >> b) & 1) ? bal : ~bal;
+        if (w == 0 && num_seqs <= 64 && NQ < 64) {
+            // One sequence per lane, all in registers: more[v] = sequences with a tile count
+            // above v from one ballot per v; a sequence's place in the order (decreasing tile
+            // count, then index) is more[its count] plus the lanes of equal count below it;
+            // the level offsets are a prefix sum over the lanes.
+            const int n = lane < num_seqs ? seq_tiles(lane) : 0;
+            const uint64_t below = (1ull << lane) - 1;
+            int more_v = 0, more_rev = 0, more_n = 0, eq_rank = 0;
+            for (int v = 0; v <= NQ; v++) {
+                const int mv = __popcll(__ballot(n > v));
+                const uint64_t eq = __ballot(n == v);
+                if (lane == v) more_v = mv;
+                if (lane == NQ - 1 - v) more_rev = mv;
+                if (n == v) {
+                    more_n = mv;
+                    eq_rank = __popcll(eq & below);
                 }
-                const int rank = __popcll(same & ((1ull << lane) - 1));
-                const int fill = sched_fill[n];
-                if (n > 0) sched_order[sched_more[n] + fill + rank] = sq;
-                if (rank == 0) sched_fill[n] = fill + __popcll(same);
-                __builtin_amdgcn_wave_barrier();
             }
+            if (lane <= NQ) sched_more[lane] = more_v;
+            if (n > 0) sched_order[more_n + eq_rank] = lane;
             // level L (tile qt = NQ-1-L) holds the sequences with more than qt tiles:
             // sched_cum[L] = sequences on the levels before L
-            const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
-                                    [&](int L, int x) { sched_cum[L] = x; }, false);
-            if (lane == 0) sched_cum[NQ] = t;
+            const int x = lane < NQ ? more_rev : 0;
+            const int incl = wave_incl_sum(x);
+            if (lane < NQ) sched_cum[lane] = incl - x;
+            if (lane == 63) sched_cum[NQ] = incl;
+        } else if (w == 0) {
+                // Wave 0 alone, without barriers (a wave's LDS operations complete in order):
+                // histogram of tile counts, more[v] = sequences with a tile count above v (its
+                // suffix sum), a stable counting sort by decreasing tile count, and the level
+                // offsets.
+                for (int v = lane; v <= NQ; v += 64) sched_fill[v] = 0;
+                __builtin_amdgcn_wave_barrier();
+                for (int sq = lane; sq < num_seqs; sq += 64) atomicAdd(&sched_fill[seq_tiles(sq)], 1);
+                __builtin_amdgcn_wave_barrier();
+                wave_scan(NQ + 1, [&](int v) { return sched_fill[v]; },
+                          [&](int v, int x) { sched_more[v] = x; }, true);
+                __builtin_amdgcn_wave_barrier();
+                for (int v = lane; v <= NQ; v += 64) sched_fill[v] = 0;
+                __builtin_amdgcn_wave_barrier();
+                // stable counting sort (every workgroup must build the same order): 64 sequences
+                // at a time, a lane's rank among equal tile counts comes from ballots over the
+                // count's bits (counts are at most PF_MAX_LEVELS < 1024)
+                for (int base = 0; base < num_seqs; base += 64) {
+                    const int sq = base + lane;
+                    const int n = sq < num_seqs ? seq_tiles(sq) : 0;
+                    uint64_t same = ~0ull;
+#pragma unroll
+                    for (int b = 0; b < 10; b++) {
+                        const uint64_t bal = __ballot((n >> b) & 1);
+                        same &= ((n >> b) & 1) ? bal : ~bal;
+                    }
+                    const int rank = __popcll(same & ((1ull << lane) - 1));
+                    const int fill = sched_fill[n];
+                    if (n > 0) sched_order[sched_more[n] + fill + rank] = sq;
+                    if (rank == 0) sched_fill[n] = fill + __popcll(same);
+                    __builtin_amdgcn_wave_barrier();
+                }
+                // level L (tile qt = NQ-1-L) holds the sequences with more than qt tiles:
+                // sched_cum[L] = sequences on the levels before L
+                const int t = wave_scan(NQ, [&](int L) { return sched_more[NQ - 1 - L]; },
+                                        [&](int L, int x) { sched_cum[L] = x; }, false);
+                if (lane == 0) sched_cum[NQ] = t;
         }
         __syncthreads();
         total_base = __builtin_amdgcn_readfirstlane(sched_cum[NQ]);
