@@ -72,6 +72,14 @@ int launch_attn_generic(int dtype, int out_dtype, void* out, int64_t o_st, int64
 
 static constexpr int PF_D = 128;   // head dims of the matrix-core path: 128 and PF_D64
 static constexpr int PF_D64 = 64;
+// a / d for 0 <= a < 2^20 and 0 < d < 2^20: a float estimate (its error is below one) and one
+// correction step; a few instructions where an integer division by a runtime value takes ~30.
+__device__ __forceinline__ int div_small(int a, int d) {
+    const int q = (int)((float)a * __builtin_amdgcn_rcpf((float)d));
+    const int r = a - q * d;
+    return q + (r >= d ? 1 : 0) - (r < 0 ? 1 : 0);
+}
+
 static constexpr int PF_QT = 128;  // query rows per head per workgroup (4 waves x 32)
 static constexpr int PF_KT = 64;   // kv tokens per tile
 static constexpr int PF_WAVES = 8; // two query heads of one kv head x 4 waves
@@ -337,7 +345,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
     int wg_items = 0;
     // the snake's share of workgroup wg in a list of n items
     auto items_of_wg = [&](int n) {
-        const int rounds = n / G, rem = n - rounds * G;
+        const int rounds = div_small(n, G), rem = n - rounds * G;
         return min(rounds + (((rounds & 1) ? G - 1 - wg : wg) < rem ? 1 : 0), PF_MAX_WG_ITEMS);
     };
     // item k of this workgroup: tile NQ-1-level of sequence seq, heads h0 .. of kv head kvh
@@ -527,11 +535,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
                         lg = 0;
                         level = L + 1;
                     } else if (lg == 1) {
-                        kvh = p / half_rep;
+                        kvh = div_small(p, half_rep);
                         h0 = 2 * (p - kvh * half_rep);
                     } else {
                         const int g = (n_rep + (1 << lg) - 1) >> lg;  // items per kv head
-                        kvh = p / g;
+                        kvh = div_small(p, g);
                         h0 = (p - kvh * g) << lg;
                     }
                 }
@@ -552,7 +560,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 #pragma unroll
                 for (int part = 0; part < 2; part++) {
                     const int a = part ? a2 : a1, c = part ? x.c2 : x.c1;
-                    for (int rd = a / G; rd * G < a + c && rd < wg_items; rd++) {
+                    for (int rd = div_small(a, G); rd * G < a + c && rd < wg_items; rd++) {
                         const int idx = rd * G + ((rd & 1) ? G - 1 - wg : wg);
                         if (idx >= a && idx < a + c) put_entry_item(rd, part, idx - a, x);
                     }
@@ -575,7 +583,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void varlen_prefill_mfma_kernel(
 #pragma unroll
                 for (int part = 0; part < 2; part++) {
                     const int a = part ? a2 : a1, end = min(a + (part ? x.c2 : x.c1), cut);
-                    for (int rd = a / G; rd * G < end; rd++) {
+                    for (int rd = div_small(a, G); rd * G < end; rd++) {
                         const int p0 = max(a, rd * G) - rd * G, p1 = min(end, rd * G + G) - rd * G;
                         atomicAdd(&sched_load[(rd & 1) ? G - p1 : p0], cost);
                         atomicAdd(&sched_load[(rd & 1) ? G - p0 : p1], -cost);
