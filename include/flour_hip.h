@@ -27,7 +27,9 @@
  *     cores with V converted to fp16 (exact for 2^-17 <= |v| <= 65504) and P rounded to fp16;
  *     a work item whose output is not finite or whose output block has a root mean square
  *     below 2^-25 / 5e-4 (~6e-5) is recomputed with bf16 V and P split into two bf16 parts.
- *     Decode splits P into two 16-bit parts.
+ *     Decode splits P into two 16-bit parts. fp32 pools stay fp32 throughout: prefill at
+ *     head_dim 64 / 128 runs on the fp32 matrix cores, every other fp32 shape on the vector
+ *     ALUs.
  */
 #ifndef FLOUR_HIP_H
 #define FLOUR_HIP_H
