@@ -34,8 +34,9 @@ namespace flour {
 
 static constexpr int F32M_QT = 32;  // query rows per workgroup
 static constexpr int F32M_KT = 32;  // kv positions per step
-// Waves per workgroup: at head_dim 64 a wave holds ~170 registers, so two waves share a SIMD;
-// at 128 it holds ~300 and runs alone on its SIMD.
+// Waves per workgroup: at head_dim 64 a wave holds 128 registers (two per SIMD, and two
+// workgroups per CU); at 128 it holds 256, one per SIMD (8 waves of ~200 registers measured
+// slower).
 __host__ __device__ constexpr int f32m_waves(int d) { return d == 64 ? 8 : 4; }
 
 __device__ __forceinline__ f32x16 mfma32x32x2_f32(float a, float b, f32x16 c) {
