@@ -354,6 +354,41 @@ def test_prefill_persistent_schedule_matches_one_workgroup_per_tile(device, H, G
     assert max_abs <= 2e-3 and rel <= 1e-3
 
 
+@pytest.mark.parametrize("n,max_len", [(64, 8064), (65, 900), (30, 8065)])
+def test_prefill_schedule_order_on_both_sort_paths(device, n, max_len):
+    """The sequence order of the persistent schedule is built in registers for up to 64
+    sequences and 63 tiles, through LDS otherwise; on both sides of each limit (64 sequences
+    with one of 63 tiles; 65 sequences; 64 tiles) the output is bit-identical to one workgroup
+    per item, with equal tile counts (ties broken by index) and empty sequences."""
+    from flour_amd import _lib
+    rng = np.random.default_rng(n)
+    lens = [int(x) for x in rng.integers(0, 400, size=n)]
+    lens[0] = max_len
+    lens[1] = 0
+    lens[2] = lens[3] = 256  # equal tile counts
+    c = make_prefill(n, 8, 2, 128, 16, (1, 1), prefix=0, dtype=torch.bfloat16, seed=n + 1,
+                     device=device, q_lens=lens)
+    write(c)
+
+    def go(persistent):
+        out = torch.full((c.q.shape[0], 8, 128), 7.0, dtype=torch.float32, device=device)
+        _lib.lib().flour_hip_set_prefill_persistent(persistent)
+        try:
+            ops.varlen_prefill(c.q, c.k_pool, c.v_pool, c.cu_seqlens_q, c.kv_lens,
+                               c.block_tables, c.max_seqlen_q, c.scale, out_dtype=torch.float32,
+                               out=out)
+            torch.cuda.synchronize()
+        finally:
+            _lib.lib().flour_hip_set_prefill_persistent(1)
+        return out
+
+    a, b = go(1), go(0)
+    assert torch.equal(a, b)
+    ref, rows = oracle_prefill(c, seqs=[2, 3, n - 1])
+    max_abs, rel = errors(to_np(a)[rows], ref)
+    assert max_abs <= 2e-3 and rel <= 1e-3
+
+
 @pytest.mark.parametrize("H,G", [(20, 4), (28, 4), (32, 4)])
 def test_prefill_partial_tile_shapes(device, H, G):
     """A sequence's last query tile with at most 64 (32) rows runs as items of 4 (8) heads x
